@@ -1,0 +1,185 @@
+"""int4 g128 (scale + min) weights and the GEMM, restated from the reference in numpy.
+
+bf16/fp16 tensors are held as float32 arrays whose values are exactly representable in
+that format; *_bits helpers convert to and from the 16-bit patterns.
+
+Pinning:
+  f32_to_bf16_bits / bf16_round  -- known-answer values (tests/test_oracle_int4.py) and torch's
+                                    own bf16 cast on CPU (a library routine, not the reference).
+  unpack_int4, pack_engine       -- closed form; round trip; hand-built bytes.
+  dequantize_int4                -- hand-computed two-rounding cases; torch CPU bf16 in-place
+                                    mul/add (the very ops quant.py:47-53 runs).
+  quantize_int4                  -- RTN bound |w - deq| <= s/2 + bf16 rounding; exact round trip
+                                    on weights built from codes.
+  gemm_exact / gemm_dequant      -- brute-force triple loop on tiny shapes; fp64 matmul.
+  gemm_fold                      -- equals gemm_exact within fp32 error (algebraic identity).
+  pack_strip                     -- our own layout (not the reference's): its definition is
+                                    checked by a per-element brute force and by unpack_strip.
+"""
+import numpy as np
+
+GROUP = 128
+
+
+# ------------------------------------------------------------------ 16-bit float helpers
+
+def f32_to_bf16_bits(a) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round(a) -> np.ndarray:
+    return bf16_bits_to_f32(f32_to_bf16_bits(a))
+
+
+def f16_round(a) -> np.ndarray:
+    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def round_to(a, dtype: str) -> np.ndarray:
+    return bf16_round(a) if dtype == "bf16" else f16_round(a)
+
+
+def to_bits(a, dtype: str) -> np.ndarray:
+    return f32_to_bf16_bits(a) if dtype == "bf16" else np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def from_bits(b, dtype: str) -> np.ndarray:
+    return bf16_bits_to_f32(b) if dtype == "bf16" else np.asarray(b, np.uint16).view(np.float16).astype(np.float32)
+
+
+# ------------------------------------------------------------------ packing
+
+def unpack_int4(packed: np.ndarray) -> np.ndarray:
+    """uint8 [N, K/2] -> codes uint8 [N, K]; element 2j is the low nibble of byte j
+    (reference tokenrush/quant.py:39-44)."""
+    lo = packed & 0xF
+    hi = packed >> 4
+    return np.stack([lo, hi], axis=-1).reshape(packed.shape[0], -1)
+
+
+def pack_engine(codes: np.ndarray) -> np.ndarray:
+    """codes uint8 [N, K] (0..15) -> uint8 [N, K/2] (reference tokenrush/quant.py:34-35)."""
+    c = codes.reshape(codes.shape[0], -1, 2).astype(np.uint8)
+    return (c[..., 0] | (c[..., 1] << 4)).astype(np.uint8)
+
+
+# nibble p of a strip-layout word holds element NIBBLE_K[p] of its 8-element run
+NIBBLE_K = np.array([0, 2, 4, 6, 1, 3, 5, 7])
+
+
+def pack_strip(packed: np.ndarray) -> np.ndarray:
+    """Engine packing -> the gfx950 strip layout uint8 [N/16, G, 64, 16] (the layout
+    token-rush_amd/csrc/int4_gemm.hip documents; it has no counterpart in the reference, whose
+    load-time repack is Marlin's, marlin.py:73-96)."""
+    codes = unpack_int4(packed).astype(np.uint32)
+    N, K = codes.shape
+    S, G = N // 16, K // GROUP
+    a = codes.reshape(S, 16, G, 4, 4, 8)                 # strip, n, g, c, j, kk
+    a = a.transpose(0, 2, 3, 1, 4, 5).reshape(S, G, 64, 4, 8)   # lane = 16 c + n
+    words = np.zeros((S, G, 64, 4), dtype=np.uint32)
+    for p in range(8):
+        words |= a[..., NIBBLE_K[p]] << np.uint32(4 * p)
+    return words.view(np.uint8).reshape(S, G, 64, 16)
+
+
+def unpack_strip(strip: np.ndarray) -> np.ndarray:
+    """Inverse of pack_strip -> engine packing uint8 [N, K/2]."""
+    S, G = strip.shape[:2]
+    words = np.ascontiguousarray(strip).view(np.uint32).reshape(S, G, 64, 4)
+    a = np.zeros((S, G, 64, 4, 8), dtype=np.uint32)
+    for p in range(8):
+        a[..., NIBBLE_K[p]] = (words >> np.uint32(4 * p)) & 0xF
+    a = a.reshape(S, G, 4, 16, 4, 8).transpose(0, 3, 1, 2, 4, 5).reshape(S * 16, G * GROUP)
+    return pack_engine(a.astype(np.uint8))
+
+
+# ------------------------------------------------------------------ quantize / dequantize
+
+def quantize_int4(w: np.ndarray, group: int = GROUP):
+    """bf16-valued [N, K] -> (packed uint8 [N, K/2], scale, mn) (bf16-valued float32).
+    Reference tokenrush/quant.py:20-36: per-group min/max, scale = (max-min)/15 (0 -> 1), both
+    rounded to bf16 first, codes = clamp(round((w - mn)/scale), 0, 15)."""
+    N, K = w.shape
+    wf = w.astype(np.float32).reshape(N, K // group, group)
+    mn = wf.min(-1)
+    scale = (wf.max(-1) - mn) / np.float32(15.0)
+    scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
+    scale, mn = bf16_round(scale), bf16_round(mn)
+    q = np.clip(np.rint((wf - mn[..., None]) / scale[..., None]), 0, 15).astype(np.uint8)
+    return pack_engine(q.reshape(N, K)), scale, mn
+
+
+def dequantize_int4(packed: np.ndarray, scale: np.ndarray, mn: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """-> [N, K] float32 holding round(round(q * s) + m) in `dtype` (reference
+    tokenrush/quant.py:47-53: in-place bf16 mul_ then add_, each computed in fp32 and rounded).
+    For fp16 parameters the same two roundings happen in fp16."""
+    codes = unpack_int4(packed).astype(np.float32)
+    N, K = codes.shape
+    G = scale.shape[1]
+    c = codes.reshape(N, G, K // G)
+    t = round_to(c * scale.astype(np.float32)[..., None], dtype)
+    return round_to(t + mn.astype(np.float32)[..., None], dtype).reshape(N, K)
+
+
+# ------------------------------------------------------------------ the GEMM
+
+def weights_f64(packed, scale, mn) -> np.ndarray:
+    """The exact dense weight q * s + m in float64 (no intermediate rounding)."""
+    codes = unpack_int4(packed).astype(np.float64)
+    N, K = codes.shape
+    G = scale.shape[1]
+    w = codes.reshape(N, G, K // G) * scale.astype(np.float64)[..., None] + mn.astype(np.float64)[..., None]
+    return w.reshape(N, K)
+
+
+def gemm_exact(x, packed, scale, mn) -> np.ndarray:
+    """y = x . (q s + m)^T in float64: the mathematical product the kernels approximate."""
+    return x.astype(np.float64) @ weights_f64(packed, scale, mn).T
+
+
+def gemm_dequant(x, packed, scale, mn, dtype: str = "bf16") -> np.ndarray:
+    """The reference's torch path: x.float() @ dequantize_int4(q, s, m).float().t()
+    (tokenrush/quant.py:373-374; the `ref` of tests/test_marlin.py:33), in float64."""
+    return x.astype(np.float64) @ dequantize_int4(packed, scale, mn, dtype).astype(np.float64).T
+
+
+def gemm_fold(x, packed, scale, mn) -> np.ndarray:
+    """The per-(row, group) fold s * sum(q x) + m * sum(x) in fp32 (reference
+    tokenrush/quant.py:113-119, the Triton GEMV's inner step), accumulated over groups in order."""
+    codes = unpack_int4(packed).astype(np.float32)
+    N, K = codes.shape
+    G = scale.shape[1]
+    xf = x.astype(np.float32)
+    M = xf.shape[0]
+    acc = np.zeros((M, N), dtype=np.float32)
+    for g in range(G):
+        sl = slice(g * (K // G), (g + 1) * (K // G))
+        qx = (xf[:, sl] @ codes[:, sl].T).astype(np.float32)          # [M, N]
+        xs = xf[:, sl].sum(-1, dtype=np.float32)[:, None]              # [M, 1]
+        acc = acc + scale[:, g][None, :].astype(np.float32) * qx + mn[:, g][None, :].astype(np.float32) * xs
+    return acc
+
+
+# ------------------------------------------------------------------ synthetic inputs
+
+def make_weights(N: int, K: int, seed: int, dtype: str = "fp16"):
+    """Codes uniform in 0..15 (engine packing), scale ~U(0.002, 0.02), min ~U(-0.15, -0.01),
+    rounded to `dtype`."""
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    scale = round_to(rng.uniform(0.002, 0.02, size=(N, K // GROUP)).astype(np.float32), dtype)
+    mn = round_to(rng.uniform(-0.15, -0.01, size=(N, K // GROUP)).astype(np.float32), dtype)
+    return pack_engine(codes), scale, mn
+
+
+def make_x(M: int, K: int, seed: int) -> np.ndarray:
+    """bf16-valued activations ~N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    return bf16_round(rng.standard_normal((M, K)).astype(np.float32))

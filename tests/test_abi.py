@@ -1,0 +1,53 @@
+"""The C-ABI library loads and exports every symbol include/*.h declares (no GPU calls)."""
+import ctypes
+import glob
+import os
+import re
+
+from conftest import ROOT
+
+
+def _declared():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        src = open(h).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        names |= set(re.findall(r"\bint\s+(tr_\w+)\s*\(", src))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert {"tr_int4_gemm", "tr_pack_int4", "tr_partial_slots"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    from tokenrush_amd import _lib
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in sorted(_declared()) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_signatures_cover_header():
+    from tokenrush_amd import _lib
+    assert _declared() == set(_lib.SIGNATURES), set(_lib.SIGNATURES) ^ _declared()
+
+
+def test_plan_is_host_only_and_independent_of_m():
+    from tokenrush_amd import gfx950
+    for N, K in [(5120, 5120), (7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (248320, 5120), (16, 128)]:
+        T, W, S = gfx950.plan(N, K)
+        assert (N // 16) % T == 0 and 1 <= W <= 8 and S == 1
+        assert gfx950.ext().tr_partial_slots(N, K, 1) == gfx950.ext().tr_partial_slots(N, K, 32) == S
+
+
+def test_shape_errors_are_codes_not_crashes():
+    from tokenrush_amd import _lib
+    lib = _lib.lib()
+    # rejected before any HIP call: null pointers / bad shapes
+    assert lib.tr_int4_gemm(None, None, None, None, None, None, 8, 100, 5120, 128, 0, 0, None) == _lib.ERR_SHAPE
+    assert lib.tr_int4_gemm(None, None, None, None, None, None, 33, 128, 5120, 128, 0, 0, None) == _lib.ERR_SHAPE
+    assert lib.tr_int4_gemm(None, None, None, None, None, None, 8, 128, 5120, 64, 0, 0, None) == _lib.ERR_CONFIG
+    assert lib.tr_int4_gemm(None, None, None, None, None, None, 8, 128, 5120, 128, 0, 0, None) == _lib.ERR_ARG
+    assert lib.tr_pack_int4(None, None, 16, 128, None) == _lib.ERR_ARG
+    assert lib.tr_partial_slots(100, 128, 1) == -1

@@ -1,0 +1,221 @@
+"""Parity of the gfx950 int4 verify GEMM with the CPU oracle (oracle/int4.py), called through
+the C-ABI (tokenrush_amd.gfx950 -> libtrhip.so). Mirrors the reference's tests/test_marlin.py:
+the same shapes and M values, its tolerance (max-abs <= max|ref| * 2^-7, test_marlin.py:35-36),
+rows independent of M (:42-52), graph replay == eager (:55-72), partials sum to the product
+(:75-87); plus a tight bound, the fp16 benchmark format and M up to 32."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4 as o
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def dev_weights(p, s, m, dtype):
+    d = torch.device("cuda:0")
+    return (torch.from_numpy(p).to(d), torch.from_numpy(s).to(TDT[dtype]).to(d),
+            torch.from_numpy(m).to(TDT[dtype]).to(d))
+
+
+def dev_x(x):
+    return torch.from_numpy(x).to(torch.bfloat16).to("cuda:0")
+
+
+def check_close(y: torch.Tensor, ref: np.ndarray, what=""):
+    y = y.float().cpu().numpy().astype(np.float64)
+    err = np.abs(y - ref)
+    amax = np.abs(ref).max()
+    assert err.max() <= amax * 2 ** -7, (what, err.max(), amax)                      # reference bar
+    assert np.linalg.norm(y - ref) <= 1e-2 * np.linalg.norm(ref), what
+    # tight: bf16 output rounding (2^-9 relative) plus fp32 accumulation noise
+    assert np.all(err <= np.abs(ref) * 2 ** -8 + amax * 2 ** -14), (what, (err - np.abs(ref) * 2 ** -8).max())
+
+
+@pytest.mark.parametrize("N,K", [(5120, 6144), (256, 5120), (1280, 5120), (5120, 17408)])
+def test_pack_matches_oracle(dev, N, K):
+    from tokenrush_amd import gfx950
+    say(f"pack N={N} K={K}")
+    p, s, m = o.make_weights(N, K, seed=0, dtype="bf16")
+    q, sd, md = dev_weights(p, s, m, "bf16")
+    B, sp, mp = gfx950.pack(q, sd, md)
+    torch.cuda.synchronize()
+    assert B.shape == (N // 16, K // 128, 64, 16)
+    assert np.array_equal(B.cpu().numpy(), o.pack_strip(p))
+    q2, s2, m2 = gfx950.unpack(B, sp, mp)
+    assert torch.equal(q, q2) and torch.equal(sd, s2) and torch.equal(md, m2)
+
+
+@pytest.mark.parametrize("N,K", [(5120, 6144), (256, 5120), (1280, 5120), (14336, 5120), (5120, 17408)])
+@pytest.mark.parametrize("M", [1, 3, 8, 16])
+def test_mul_matches_oracle(dev, N, K, M):
+    from tokenrush_amd import gfx950
+    say(f"mul N={N} K={K} M={M}")
+    p, s, m = o.make_weights(N, K, seed=1, dtype="bf16")
+    x = o.make_x(M, K, seed=2)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "bf16"))
+    y = gfx950.mul(dev_x(x), B, sp, mp)
+    torch.cuda.synchronize()
+    check_close(y, o.gemm_exact(x, p, s, m), f"N={N} K={K} M={M}")
+
+
+@pytest.mark.parametrize("M", [17, 24, 32])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_mul_two_row_tiles(dev, M, dtype):
+    from tokenrush_amd import gfx950
+    say(f"mul M={M} {dtype}")
+    p, s, m = o.make_weights(1280, 5120, seed=3, dtype=dtype)
+    x = o.make_x(M, 5120, seed=4)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, dtype))
+    y = gfx950.mul(dev_x(x), B, sp, mp)
+    torch.cuda.synchronize()
+    check_close(y, o.gemm_exact(x, p, s, m), f"M={M}")
+
+
+@pytest.mark.parametrize("T,W", [(1, 1), (1, 3), (2, 2), (2, 8), (4, 1), (4, 5)])
+def test_tilings_agree(dev, T, W):
+    from tokenrush_amd import gfx950
+    say(f"tiling T={T} W={W}")
+    p, s, m = o.make_weights(512, 6144, seed=5, dtype="fp16")
+    x = o.make_x(8, 6144, seed=6)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "fp16"))
+    y = gfx950.mul(dev_x(x), B, sp, mp, thread_t=T, thread_w=W)
+    torch.cuda.synchronize()
+    check_close(y, o.gemm_exact(x, p, s, m), f"T={T} W={W}")
+
+
+def test_rows_independent_of_m(dev):
+    """Row i of an M-row call is bit-identical whatever M is (reference test_marlin.py:42-52)."""
+    from tokenrush_amd import gfx950
+    say("rows independent of M")
+    p, s, m = o.make_weights(5120, 17408, seed=7, dtype="bf16")
+    x = dev_x(o.make_x(32, 17408, seed=8))
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "bf16"))
+    y32 = gfx950.mul(x, B, sp, mp)
+    for M in (1, 3, 8, 16, 17):
+        yM = gfx950.mul(x[:M].contiguous(), B, sp, mp)
+        assert torch.equal(yM, y32[:M]), M
+
+
+def test_repeat_is_deterministic(dev):
+    from tokenrush_amd import gfx950
+    say("determinism")
+    p, s, m = o.make_weights(7168, 5120, seed=9, dtype="fp16")
+    x = dev_x(o.make_x(8, 5120, seed=10))
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "fp16"))
+    y0 = gfx950.mul(x, B, sp, mp)
+    for _ in range(5):
+        assert torch.equal(gfx950.mul(x, B, sp, mp), y0)
+
+
+def test_graph_replay_matches_eager(dev):
+    """Reference test_marlin.py:55-72, replayed several times with eager work in between."""
+    from tokenrush_amd import gfx950
+    say("graph replay")
+    p, s, m = o.make_weights(1280, 5120, seed=11, dtype="bf16")
+    x = dev_x(o.make_x(4, 5120, seed=12))
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "bf16"))
+    y = gfx950.mul(x, B, sp, mp)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        out = gfx950.mul(x, B, sp, mp)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out.copy_(gfx950.mul(x, B, sp, mp))
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y), i
+        _ = gfx950.mul(x, B, sp, mp)        # eager work between replays
+
+
+@pytest.mark.parametrize("N,K", [(5120, 6144), (5120, 17408), (256, 5120)])
+@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("slots", [None, 3])
+def test_partials_sum_to_product(dev, N, K, M, slots):
+    """Reference test_marlin.py:75-87: every slot written, the sum is the product."""
+    from tokenrush_amd import gfx950
+    say(f"partials N={N} K={K} M={M} slots={slots}")
+    p, s, m = o.make_weights(N, K, seed=13, dtype="bf16")
+    x = o.make_x(M, K, seed=14)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "bf16"))
+    xd = dev_x(x)
+    y = gfx950.mul(xd, B, sp, mp)
+    part = gfx950.mul_partial(xd, B, sp, mp, n_slots=slots)
+    assert part.shape[1:] == (M, N) and part.shape[0] == (slots or gfx950.partial_slots(N, K))
+    ref = o.gemm_exact(x, p, s, m)
+    tot = part.sum(0).double().cpu().numpy()
+    assert np.abs(tot - ref).max() <= np.abs(ref).max() * 2 ** -7
+    assert (part.sum(0).to(torch.bfloat16).float() - y.float()).abs().max().item() <= np.abs(ref).max() * 2 ** -7
+    part2 = torch.full_like(part, float("nan"))
+    part2.copy_(gfx950.mul_partial(xd, B, sp, mp, n_slots=slots))
+    assert torch.equal(part, part2)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_dequant_bit_exact(dev, dtype):
+    from tokenrush_amd import gfx950
+    say(f"dequant {dtype}")
+    p, s, m = o.make_weights(256, 5120, seed=15, dtype=dtype)
+    w = gfx950.dequantize(*dev_weights(p, s, m, dtype))
+    assert np.array_equal(w.float().cpu().numpy(), o.dequantize_int4(p, s, m, dtype))
+
+
+def test_config1_full_size(dev):
+    """M=1, 5120 x 5120, fp16 scale/min."""
+    from tokenrush_amd import gfx950
+    say("config1")
+    p, s, m = o.make_weights(5120, 5120, seed=101, dtype="fp16")
+    x = o.make_x(1, 5120, seed=102)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "fp16"))
+    check_close(gfx950.mul(dev_x(x), B, sp, mp), o.gemm_exact(x, p, s, m), "config1")
+
+
+@pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
+def test_config2_layer_set_m8(dev, N, K):
+    """one layer's projection set at M=8, fp16 scale/min, full size."""
+    from tokenrush_amd import gfx950
+    say(f"config2 N={N} K={K}")
+    p, s, m = o.make_weights(N, K, seed=200 + N % 97, dtype="fp16")
+    x = o.make_x(8, K, seed=201)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "fp16"))
+    check_close(gfx950.mul(dev_x(x), B, sp, mp), o.gemm_exact(x, p, s, m), f"config2 {N}x{K}")
+
+
+def test_qlinear_api(dev):
+    """The reference QLinear surface: __call__, partials, nibbles, rows, cat, dequantize,
+    nbytes, shape, and the T > MAX_ROWS prefill path."""
+    from tokenrush_amd.quant import QLinear
+    say("qlinear api")
+    p, s, m = o.make_weights(512, 1024, seed=16, dtype="bf16")
+    qd, sd, md = dev_weights(p, s, m, "bf16")
+    lin = QLinear(qd, sd, md, split_k=4)
+    assert lin.shape == (512, 1024) and lin.backend == "gfx950" and lin.group == 128
+    assert lin.nbytes == 512 * 512 + 2 * 2 * 512 * 8
+    x = o.make_x(8, 1024, seed=17)
+    ref = o.gemm_exact(x, p, s, m)
+    check_close(lin(dev_x(x)), ref, "call")
+    part = lin.partials(dev_x(x))
+    assert part.dtype == torch.float32 and part.shape[1:] == (8, 512)
+    q2, s2, m2 = lin.nibbles()
+    assert torch.equal(q2, qd) and torch.equal(s2, sd) and torch.equal(m2, md)
+    ids = torch.tensor([5, 17, 300, 511, 0, 1, 2, 3, 4, 6, 7, 8, 9, 10, 11, 12], device="cuda")
+    sub = lin.rows(ids)
+    check_close(sub(dev_x(x)), ref[:, ids.cpu().numpy()], "rows")
+    both = QLinear.cat([lin, sub])
+    assert both.shape == (528, 1024)
+    assert torch.equal(lin.dequantize().float().cpu(), torch.from_numpy(o.dequantize_int4(p, s, m)))
+    xl = o.make_x(40, 1024, seed=18)                  # T > 32: dequant + matmul (prefill path)
+    y = lin(dev_x(xl)).float().cpu().numpy()
+    r = o.gemm_dequant(xl, p, s, m)
+    assert np.abs(y - r).max() <= np.abs(r).max() * 2 ** -7

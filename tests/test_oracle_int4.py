@@ -1,0 +1,120 @@
+"""Pins the numpy oracle for the int4 weights and GEMM (oracle/int4.py) against known
+answers, torch's own CPU bf16/fp16 arithmetic (the ops the reference's dequantize runs),
+brute force on tiny inputs, and algebraic identities. No GPU."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4 as o
+
+
+def test_bf16_rounding_known_answers():
+    vals = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 1.0 + 2 ** -8 + 2 ** -20, -2.5, 0.0, 65504.0, 3e38],
+                    dtype=np.float32)
+    bits = o.f32_to_bf16_bits(vals)
+    # 1+2^-8 is a tie -> even (0x3F80); 1+3*2^-8 is a tie -> even (0x3F82); just above a tie rounds up
+    assert bits.tolist() == [0x3F80, 0x3F80, 0x3F82, 0x3F81, 0xC020, 0x0000, 0x4780, 0x7F62]
+
+
+def test_bf16_rounding_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    a = (rng.standard_normal(100000) * 10 ** rng.uniform(-6, 6, 100000)).astype(np.float32)
+    ref = torch.from_numpy(a).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(o.f32_to_bf16_bits(a), ref)
+
+
+def test_unpack_known_bytes():
+    packed = np.array([[0x21, 0xF0, 0x7A]], dtype=np.uint8)
+    assert o.unpack_int4(packed).tolist() == [[1, 2, 0, 15, 10, 7]]
+    assert np.array_equal(o.pack_engine(o.unpack_int4(packed)), packed)
+
+
+def test_dequant_two_roundings_hand_case():
+    # q = 15, s = bf16(0.0123) -> q*s rounds to bf16, then + m rounds again
+    s = o.bf16_round(np.float32(0.0123)).reshape(1, 1)
+    m = o.bf16_round(np.float32(-0.1)).reshape(1, 1)
+    packed = np.full((1, 64), 0xFF, dtype=np.uint8)
+    w = o.dequantize_int4(packed, s, m)
+    t = o.bf16_round(np.float32(15) * s[0, 0])
+    assert w[0, 0] == o.bf16_round(t + m[0, 0])
+    # single rounding would differ here: the two-rounding result is what the reference computes
+    assert np.all(w == w[0, 0])
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_dequant_matches_torch_inplace_ops(dtype):
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    p, s, m = o.make_weights(64, 512, seed=3, dtype=dtype)
+    codes = torch.from_numpy(o.unpack_int4(p).astype(np.int64))
+    w = codes.to(tdt).view(64, 4, 128)
+    w.mul_(torch.from_numpy(s).to(tdt)[..., None]).add_(torch.from_numpy(m).to(tdt)[..., None])
+    assert np.array_equal(w.float().view(64, 512).numpy(), o.dequantize_int4(p, s, m, dtype))
+
+
+def test_quantize_roundtrip_and_bound():
+    rng = np.random.default_rng(1)
+    w = o.bf16_round(rng.standard_normal((32, 256)).astype(np.float32) * 0.02)
+    p, s, m = o.quantize_int4(w)
+    deq = o.dequantize_int4(p, s, m)
+    err = np.abs(deq - w).reshape(32, 2, 128)
+    assert np.all(err <= s[..., None] / 2 + np.abs(w).reshape(32, 2, 128).max() * 2 ** -7 + 1e-6)
+    # the codes chosen are the nearest: no other code is closer to w
+    codes = o.unpack_int4(p).astype(np.float32).reshape(32, 2, 128)
+    wg = w.reshape(32, 2, 128)
+    for d in (-1, 1):
+        alt = np.clip(codes + d, 0, 15) * s[..., None] + m[..., None]
+        assert np.all(np.abs(alt - wg) >= np.abs(codes * s[..., None] + m[..., None] - wg) - 1e-7)
+
+
+def test_quantize_matches_torch_restatement():
+    """quant.py:20-36 run as torch CPU ops (what tests/test_marlin.py:10-14 uses to build weights)."""
+    from tokenrush_amd.quant import quantize_int4 as q_torch
+    rng = np.random.default_rng(2)
+    w = o.bf16_round(rng.standard_normal((16, 384)).astype(np.float32) * 0.02)
+    pt, st, mt = q_torch(torch.from_numpy(w).to(torch.bfloat16))
+    p, s, m = o.quantize_int4(w)
+    assert np.array_equal(pt.numpy(), p)
+    assert np.array_equal(st.float().numpy(), s) and np.array_equal(mt.float().numpy(), m)
+
+
+def test_gemm_exact_brute_force():
+    p, s, m = o.make_weights(16, 256, seed=4, dtype="bf16")
+    x = o.make_x(2, 256, seed=5)
+    codes = o.unpack_int4(p)
+    y = np.zeros((2, 16))
+    for i in range(2):
+        for n in range(16):
+            y[i, n] = sum(float(x[i, k]) * (int(codes[n, k]) * float(s[n, k // 128]) + float(m[n, k // 128]))
+                          for k in range(256))
+    assert np.allclose(o.gemm_exact(x, p, s, m), y, rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_fold_equals_exact():
+    p, s, m = o.make_weights(64, 1024, seed=6)
+    x = o.make_x(4, 1024, seed=7)
+    ref = o.gemm_exact(x, p, s, m)
+    assert np.abs(o.gemm_fold(x, p, s, m) - ref).max() <= np.abs(ref).max() * 1e-5
+
+
+def test_gemm_dequant_is_within_reference_tolerance():
+    p, s, m = o.make_weights(64, 1024, seed=8, dtype="bf16")
+    x = o.make_x(4, 1024, seed=9)
+    ref = o.gemm_exact(x, p, s, m)
+    assert np.abs(o.gemm_dequant(x, p, s, m) - ref).max() <= np.abs(ref).max() * 2 ** -7
+
+
+def test_pack_strip_per_element():
+    """The strip layout, element by element, from its definition: code (n, k) sits in tile
+    (n // 16, k // 128), lane 16 * c + n % 16 with c = (k % 128) // 32, word j = (k % 32) // 8,
+    nibble p with NIBBLE_K[p] == k % 8."""
+    p, _, _ = o.make_weights(32, 256, seed=10)
+    codes = o.unpack_int4(p)
+    st = o.pack_strip(p)
+    words = st.view(np.uint32).reshape(2, 2, 64, 4)
+    inv = {int(k): pp for pp, k in enumerate(o.NIBBLE_K)}
+    for n in range(32):
+        for k in range(256):
+            c, j = (k % 128) // 32, (k % 32) // 8
+            w = int(words[n // 16, k // 128, 16 * c + n % 16, j])
+            assert (w >> (4 * inv[k % 8])) & 0xF == codes[n, k]
+    assert np.array_equal(o.unpack_strip(st), p)
