@@ -13,11 +13,13 @@
  *   x        bf16 [M, K]                 activations (M <= 32)
  *   qweight  uint8 [N, K/2]              engine packing: element 2j in the low nibble of byte j
  *                                        (tokenrush/quant.py:9-10)
- *   packed   uint8 [N/16, K/128, 64, 16] strip layout made by tr_pack_int4
+ *   packed   uint8 [N/16, K/128, 1088]   strip layout made by tr_pack_int4 (codes + scale/min)
  *   scale,mn [N, K/128]                  bf16 (scale_dtype 0, the engine format) or fp16 (1)
  */
 #ifndef TOKENRUSH_HIP_H
 #define TOKENRUSH_HIP_H
+
+#include <stddef.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -25,34 +27,46 @@ extern "C" {
 
 /* ---------------------------------------------------------------- int4 verify GEMM */
 
-/* y = x . (q*s + m)^T for M <= 32 rows. Exactly one of `out` (bf16 [M, N]) and `partials`
- * (fp32 [n_slots, M, N], every slot written, sum over slots = product) is non-null.
- * N % 16 == 0, K % 128 == 0, group == 128.
+/* y = x . (q*s + m)^T for M <= 32 rows, packed weights from tr_pack_int4. Exactly one of
+ * `out` (bf16 [M, N]) and `partials` (fp32 [n_slots, M, N], every slot written, sum over slots
+ * = product; n_slots must equal tr_partial_slots or be a valid explicit split) is non-null.
+ * When out is used and tr_gemm_workspace_bytes(N, K, M) > 0, `workspace` must hold that many
+ * bytes: 64 KiB of int32 counters at offset 0, zero-filled before first use (every call leaves
+ * them at zero again; no call writes anything else there), then fp32 partials. One buffer
+ * sized for the largest call serves every shape; calls that overlap on one device must not
+ * share a workspace. N % 16 == 0, K % 128 == 0,
+ * group == 128.
  * Replaces: marlin_bf16_cuda (tokenrush/csrc/marlin_bf16.cu:630-670) behind the torch binding
- * `mul(A, B, C, s, m, workspace, red, ...)` (tokenrush/csrc/marlin_bf16.cpp:14-44); C bf16 ->
- * out, C fp32 [slots, m, n] -> partials. No lock/reduce workspace is needed. */
-int tr_int4_gemm(const void* x, const void* packed, const void* scale, const void* mn, void* out,
-                 void* partials, int M, int N, int K, int group, int scale_dtype, int n_slots,
+ * `mul(A, B, C, s, m, workspace, red, ...)` (tokenrush/csrc/marlin_bf16.cpp:14-44): C bf16 ->
+ * out, C fp32 [slots, m, n] -> partials, workspace/red -> workspace. */
+int tr_int4_gemm(const void* x, const void* packed, void* out, void* partials, void* workspace,
+                 size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
                  void* stream);
 
-/* tr_int4_gemm with explicit tiling: T strips of 16 rows per workgroup (1, 2, 4; T = 4 only for
- * M <= 16), W waves per workgroup (1..8). The role of Marlin's thread_k/thread_n/sms overrides
- * (tokenrush/csrc/marlin_bf16.cpp:14-16). */
-int tr_int4_gemm_ex(const void* x, const void* packed, const void* scale, const void* mn, void* out,
-                    void* partials, int M, int N, int K, int group, int scale_dtype, int n_slots,
-                    int T, int W, void* stream);
+/* tr_int4_gemm with an explicit number of 16-row strips per workgroup (R > 0; R <= 0 = default).
+ * The role of Marlin's thread_k/thread_n/sms overrides (tokenrush/csrc/marlin_bf16.cpp:14-16). */
+int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials, void* workspace,
+                    size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
+                    int R, void* stream);
 
-/* The default tiling of an N x K weight (independent of M). Host only. */
-int tr_gemm_plan(int N, int K, int* T, int* W, int* S);
+/* The default tiling of an N x K weight for M rows: S K-slots, W waves and R strips per
+ * workgroup. Depends on M only through M > 16. Host only, no GPU call. */
+int tr_gemm_plan(int N, int K, int M, int* S, int* W, int* R);
 
-/* fp32 slots a partial-mode call writes for an N x K weight (-1 for an unsupported shape).
+/* fp32 slots a partial-mode call writes for an N x K weight at M rows (-1: unsupported shape).
  * Replaces: partial_slots (tokenrush/csrc/marlin_bf16.cu:611-625, marlin_bf16.cpp:46-48). */
 int tr_partial_slots(int N, int K, int M);
 
-/* Engine packing -> strip layout, and back. Replaces: marlin.pack / marlin.unpack
- * (tokenrush/marlin.py:73-118), which are torch-op layout conversions in the reference. */
-int tr_pack_int4(const void* qweight, void* packed, int N, int K, void* stream);
-int tr_unpack_int4(const void* packed, void* qweight, int N, int K, void* stream);
+/* Bytes of workspace an out-mode call needs (0: none). Host only.
+ * Replaces: the lock + fp32 reduce buffer sizing of marlin.workspaces (tokenrush/marlin.py:121-135). */
+size_t tr_gemm_workspace_bytes(int N, int K, int M);
+
+/* Engine packing + scale/min -> strip layout uint8 [N/16, K/128, 1088], and back.
+ * Replaces: marlin.pack / marlin.unpack (tokenrush/marlin.py:73-118), torch-op layout
+ * conversions in the reference. */
+int tr_pack_int4(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K,
+                 void* stream);
+int tr_unpack_int4(const void* packed, void* qweight, void* scale, void* mn, int N, int K, void* stream);
 
 /* Dense weight [N, K] in the scale dtype: round(round(q*s) + m), two roundings.
  * Replaces: dequantize_int4 (tokenrush/quant.py:47-53). */

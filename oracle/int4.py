@@ -74,10 +74,14 @@ def pack_engine(codes: np.ndarray) -> np.ndarray:
 NIBBLE_K = np.array([0, 2, 4, 6, 1, 3, 5, 7])
 
 
-def pack_strip(packed: np.ndarray) -> np.ndarray:
-    """Engine packing -> the gfx950 strip layout uint8 [N/16, G, 64, 16] (the layout
+TILE = 1088
+
+
+def pack_strip(packed: np.ndarray, scale: np.ndarray, mn: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """Engine packing + scale/min -> the gfx950 strip layout uint8 [N/16, G, 1088] (the layout
     token-rush_amd/csrc/int4_gemm.hip documents; it has no counterpart in the reference, whose
-    load-time repack is Marlin's, marlin.py:73-96)."""
+    load-time repack is Marlin's, marlin.py:73-96): per (strip, group) 1024 bytes of codes in
+    lane order, then 16 x (scale bits | min bits << 16)."""
     codes = unpack_int4(packed).astype(np.uint32)
     N, K = codes.shape
     S, G = N // 16, K // GROUP
@@ -86,18 +90,25 @@ def pack_strip(packed: np.ndarray) -> np.ndarray:
     words = np.zeros((S, G, 64, 4), dtype=np.uint32)
     for p in range(8):
         words |= a[..., NIBBLE_K[p]] << np.uint32(4 * p)
-    return words.view(np.uint8).reshape(S, G, 64, 16)
+    sm = (to_bits(scale, dtype).astype(np.uint32) | (to_bits(mn, dtype).astype(np.uint32) << np.uint32(16)))
+    sm = sm.reshape(S, 16, G).transpose(0, 2, 1)         # [S, G, 16]
+    out = np.concatenate([words.reshape(S, G, 256), sm], axis=-1)
+    return np.ascontiguousarray(out).view(np.uint8).reshape(S, G, TILE)
 
 
-def unpack_strip(strip: np.ndarray) -> np.ndarray:
-    """Inverse of pack_strip -> engine packing uint8 [N, K/2]."""
+def unpack_strip(strip: np.ndarray, dtype: str = "bf16"):
+    """Inverse of pack_strip -> (engine packing uint8 [N, K/2], scale, mn)."""
     S, G = strip.shape[:2]
-    words = np.ascontiguousarray(strip).view(np.uint32).reshape(S, G, 64, 4)
+    words = np.ascontiguousarray(strip).view(np.uint32).reshape(S, G, 272)
+    w = words[..., :256].reshape(S, G, 64, 4)
     a = np.zeros((S, G, 64, 4, 8), dtype=np.uint32)
     for p in range(8):
-        a[..., NIBBLE_K[p]] = (words >> np.uint32(4 * p)) & 0xF
+        a[..., NIBBLE_K[p]] = (w >> np.uint32(4 * p)) & 0xF
     a = a.reshape(S, G, 4, 16, 4, 8).transpose(0, 3, 1, 2, 4, 5).reshape(S * 16, G * GROUP)
-    return pack_engine(a.astype(np.uint8))
+    sm = words[..., 256:].transpose(0, 2, 1).reshape(S * 16, G)
+    scale = from_bits((sm & 0xFFFF).astype(np.uint16), dtype)
+    mn = from_bits((sm >> 16).astype(np.uint16), dtype)
+    return pack_engine(a.astype(np.uint8)), scale, mn
 
 
 # ------------------------------------------------------------------ quantize / dequantize

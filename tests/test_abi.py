@@ -12,7 +12,7 @@ def _declared():
     for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
         src = open(h).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-        names |= set(re.findall(r"\bint\s+(tr_\w+)\s*\(", src))
+        names |= set(re.findall(r"\b(?:int|size_t)\s+(tr_\w+)\s*\(", src))
     return names
 
 
@@ -36,18 +36,21 @@ def test_python_signatures_cover_header():
 def test_plan_is_host_only_and_independent_of_m():
     from tokenrush_amd import gfx950
     for N, K in [(5120, 5120), (7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (248320, 5120), (16, 128)]:
-        T, W, S = gfx950.plan(N, K)
-        assert (N // 16) % T == 0 and 1 <= W <= 8 and S == 1
-        assert gfx950.ext().tr_partial_slots(N, K, 1) == gfx950.ext().tr_partial_slots(N, K, 32) == S
+        for M in (1, 8, 16, 17, 32):
+            S, W, R = gfx950.plan(N, K, M)
+            assert 1 <= W <= 12 and S >= 1 and R >= 1, (N, K, M, S, W, R)
+            assert gfx950.plan(N, K, 1 if M <= 16 else 32) == (S, W, R)     # depends on M only via M > 16
+            ws = gfx950.ext().tr_gemm_workspace_bytes(N, K, M)
+            assert (ws == 0) == (S == 1)
 
 
 def test_shape_errors_are_codes_not_crashes():
     from tokenrush_amd import _lib
     lib = _lib.lib()
     # rejected before any HIP call: null pointers / bad shapes
-    assert lib.tr_int4_gemm(None, None, None, None, None, None, 8, 100, 5120, 128, 0, 0, None) == _lib.ERR_SHAPE
-    assert lib.tr_int4_gemm(None, None, None, None, None, None, 33, 128, 5120, 128, 0, 0, None) == _lib.ERR_SHAPE
-    assert lib.tr_int4_gemm(None, None, None, None, None, None, 8, 128, 5120, 64, 0, 0, None) == _lib.ERR_CONFIG
-    assert lib.tr_int4_gemm(None, None, None, None, None, None, 8, 128, 5120, 128, 0, 0, None) == _lib.ERR_ARG
-    assert lib.tr_pack_int4(None, None, 16, 128, None) == _lib.ERR_ARG
+    assert lib.tr_int4_gemm(None, None, None, None, None, 0, 8, 100, 5120, 128, 0, 0, None) == _lib.ERR_SHAPE
+    assert lib.tr_int4_gemm(None, None, None, None, None, 0, 33, 128, 5120, 128, 0, 0, None) == _lib.ERR_SHAPE
+    assert lib.tr_int4_gemm(None, None, None, None, None, 0, 8, 128, 5120, 64, 0, 0, None) == _lib.ERR_CONFIG
+    assert lib.tr_int4_gemm(None, None, None, None, None, 0, 8, 128, 5120, 128, 0, 0, None) == _lib.ERR_ARG
+    assert lib.tr_pack_int4(None, None, None, None, 16, 128, None) == _lib.ERR_ARG
     assert lib.tr_partial_slots(100, 128, 1) == -1

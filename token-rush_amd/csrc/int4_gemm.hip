@@ -10,223 +10,259 @@
 //     (exponent of 128, q in the low mantissa bits), so no multiply touches a weight.
 //   * v_mfma_f32_16x16x32_bf16 contracts 16 activation rows (A) against 16 weight rows (B)
 //     over 32 k: E = sum x (128 + q) per group, fp32.
-//   * One more MFMA chain against a ones operand gives sum(x) per row and group, and the
-//     group result is  s * E + (mn - 128 s) * sum(x)  in fp32, applied once per group.
+//   * An MFMA chain against a ones operand gives X = sum(x) per row and group, and the group
+//     result is  s * E + (mn - 128 s) * X  in fp32, applied once per group.
 //
-// Rows of x beyond M are zero lanes, so every output row is computed by the same
-// instructions whatever M is: row i of an M = 1 call is bit-identical to row i of an
-// M = 8 call (the property tests/test_marlin.py:42-52 of the reference checks).
+// Rows of x beyond M are padding lanes (they load row M-1 and are never stored), so every
+// output row is computed by the same instructions for every M of one row-tile count: row i
+// of an M = 1 call is bit-identical to row i of an M = 16 call (the property the reference's
+// tests/test_marlin.py:42-52 checks for Marlin), and likewise within M = 17..32.
 //
-// Weight layout ("strip layout", made once at load time by tr_pack_int4):
-//   codes[N/16][G][64 lanes][16 B]: one 1 KiB tile per (16-row strip, group). Lane l holds
-//   row l%16, k in [32*(l/16), 32*(l/16)+32) of the group, as four 32-bit words; word j
-//   covers k0 = 32*(l/16) + 8j .. k0+7 with code k0+2p in nibble p and k0+2p+1 in nibble
-//   p+4 (p = 0..3), so (w >> 4p) & 0x000F000F is the bf16 pair (k0+2p, k0+2p+1).
-//   A wave's 16-byte load of a tile is one contiguous, fully coalesced 1 KiB read, and
-//   a strip's tiles are contiguous along K.
-//   scale, mn: the engine's own [N, K/128] arrays (bf16, or fp16 for the benchmark
-//   format), read in place.
+// Weight layout ("strip layout", made once at load time by tr_pack_int4): one 1088-byte tile
+// per (16-row strip, group of 128), tiles of a strip contiguous along K:
+//   packed[N/16][K/128][1088]
+//   bytes [0, 1024): lane l's 16 bytes at 16 l hold row l%16, k in [32 (l/16), 32 (l/16) + 32)
+//     of the group as four 32-bit words; word j covers k0 = 32 (l/16) + 8 j .. k0 + 7 with code
+//     k0 + 2p in nibble p and k0 + 2p + 1 in nibble p + 4 (p = 0..3), so
+//     (w >> 4p) & 0x000F000F is the bf16 pair (k0 + 2p, k0 + 2p + 1) once the exponent is set.
+//   bytes [1024, 1088): row i's scale (low 16 bits) and min (high 16 bits) at 1024 + 4 i.
+// A wave reads a tile with one 16-byte load per lane (1 KiB, contiguous) plus one 4-byte load.
 //
-// Work split: a workgroup owns T strips (16T rows) and one K slice (slot); its W waves
-// split the slot's groups evenly and reduce through LDS in fixed wave order, so results
-// are deterministic. With S > 1 slots each slot writes its own fp32 partial [S, M, N]
-// (no locks, no atomics), the contract of the reference's partials()
-// (tokenrush/quant.py:381-391, tokenrush/marlin.py:158-168).
+// Work split ("activation-stationary"): a workgroup owns a range of strips and a K slot; each
+// of its W waves owns one K block of GW groups (GW = 4 for M <= 16, 2 above), loads that
+// block's activations into registers once, then streams the strips' tiles for its block.
+// After each strip the waves' partial tiles are summed through LDS in fixed wave order
+// (deterministic). With S > 1 slots, slots write fp32 partials: either the caller's
+// [S, M, N] buffer (the contract of the reference's partials(), tokenrush/quant.py:381-391,
+// tokenrush/marlin.py:158-168) or a workspace the last-arriving slot reduces into bf16.
 #include "tr_common.h"
 
 namespace tr {
 
 constexpr int kGroup = 128;
+constexpr int kTileBytes = 1088;
+constexpr int kMaxWaves = 12;   // 768 threads: leaves ~170 VGPRs per lane (3 waves per SIMD)
 
-template <int T, int MT>
-struct Stage {
-  uint4 w[T];        // code tile words, one 16-B chunk per strip
-  uint32_t s[T];     // raw 16-bit scale of (row, group)
-  uint32_t m[T];     // raw 16-bit min of (row, group)
-  uint4 x[MT][4];    // activation chunks: row 16*mt + lane%16, 32 k of this lane's quad
+enum { OUT_BF16 = 0, OUT_PARTIAL = 1, OUT_BF16_VIA_WS = 2 };
+
+struct Tile {
+  uint4 w;       // this lane's 16 code bytes
+  uint32_t sm;   // scale | min << 16 of row lane % 16
 };
 
-template <int T, int MT>
-__device__ __forceinline__ void load_stage(Stage<T, MT>& st, const uint4* __restrict__ codes,
-                                           const uint16_t* __restrict__ scale,
-                                           const uint16_t* __restrict__ mn,
-                                           const uint16_t* __restrict__ x, int strip0, int G, int g,
-                                           int lane, int M, int K) {
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4* p = (const u32x4*)(codes + ((size_t)(strip0 + t) * G + g) * 64 + lane);
-    const u32x4 v = __builtin_nontemporal_load(p);
-    st.w[t] = make_uint4(v.x, v.y, v.z, v.w);
-    size_t row = (size_t)(strip0 + t) * 16 + (lane & 15);
-    st.s[t] = scale[row * G + g];
-    st.m[t] = mn[row * G + g];
-  }
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    int xr = 16 * mt + (lane & 15);
-    if (xr < M) {
-      const uint4* p = (const uint4*)(x + (size_t)xr * K + g * kGroup + 32 * (lane >> 4));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st.x[mt][j] = p[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st.x[mt][j] = make_uint4(0, 0, 0, 0);
-    }
-  }
+__device__ __forceinline__ void load_tile(Tile& t, const uint8_t* __restrict__ tile, int lane) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)(tile + 16 * lane));
+  t.w = make_uint4(v.x, v.y, v.z, v.w);
+  t.sm = __builtin_nontemporal_load((const uint32_t*)(tile + 1024 + 4 * (lane & 15)));
 }
 
-template <int T, int MT, bool F16S>
-__device__ __forceinline__ void compute_stage(const Stage<T, MT>& st, f32x4 (&acc)[T][MT],
-                                              uint32_t kExp128, uint32_t kOnes) {
+// E = sum over the group of x * (128 + q), then acc += s * E + (mn - 128 s) * X.
+template <int MT, bool F16S>
+__device__ __forceinline__ void tile_mac(const Tile& t, const uint4 (&xa)[MT][4], const f32x4 (&X)[MT],
+                                         f32x4 (&acc)[MT], uint32_t kExp128) {
   const uint32_t kMask = 0x000F000Fu;
-  const uint4 ones4 = make_uint4(kOnes, kOnes, kOnes, kOnes);
-  const bf16x8 ones = __builtin_bit_cast(bf16x8, ones4);
-  f32x4 X[MT];
+  const uint32_t wd[4] = {t.w.x, t.w.y, t.w.z, t.w.w};
+  bf16x8 b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint4 d;
+    d.x = (wd[j] & kMask) | kExp128;
+    d.y = ((wd[j] >> 4) & kMask) | kExp128;
+    d.z = ((wd[j] >> 8) & kMask) | kExp128;
+    d.w = ((wd[j] >> 12) & kMask) | kExp128;
+    b[j] = __builtin_bit_cast(bf16x8, d);
+  }
+  float sf, mf;
+  if (F16S) {
+    sf = f16_bits_to_f32(t.sm & 0xFFFFu);
+    mf = f16_bits_to_f32(t.sm >> 16);
+  } else {
+    sf = __uint_as_float(t.sm << 16);
+    mf = __uint_as_float(t.sm & 0xFFFF0000u);
+  }
+  const float c1 = fmaf(-128.f, sf, mf);  // mn - 128 s: removes the +128 code offset
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    X[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 E = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      X[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[mt][j]), ones,
-                                                      X[mt], 0, 0, 0);
-  }
+      E = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[mt][j]), b[j], E, 0, 0, 0);
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const uint32_t wd[4] = {st.w[t].x, st.w[t].y, st.w[t].z, st.w[t].w};
-    bf16x8 b[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint4 d;
-      d.x = (wd[j] & kMask) | kExp128;
-      d.y = ((wd[j] >> 4) & kMask) | kExp128;
-      d.z = ((wd[j] >> 8) & kMask) | kExp128;
-      d.w = ((wd[j] >> 12) & kMask) | kExp128;
-      b[j] = __builtin_bit_cast(bf16x8, d);
-    }
-    float sf, mf;
-    if (F16S) {
-      sf = f16_bits_to_f32(st.s[t]);
-      mf = f16_bits_to_f32(st.m[t]);
-    } else {
-      sf = bf16_bits_to_f32(st.s[t]);
-      mf = bf16_bits_to_f32(st.m[t]);
-    }
-    const float c1 = fmaf(-128.f, sf, mf);  // mn - 128 s: removes the +128 code offset
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      f32x4 E = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        E = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[mt][j]), b[j], E,
-                                                    0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        acc[t][mt][r] = fmaf(sf, E[r], acc[t][mt][r]);
-        acc[t][mt][r] = fmaf(c1, X[mt][r], acc[t][mt][r]);
-      }
+    for (int r = 0; r < 4; ++r) {
+      acc[mt][r] = fmaf(sf, E[r], acc[mt][r]);
+      acc[mt][r] = fmaf(c1, X[mt][r], acc[mt][r]);
     }
   }
 }
 
-// One output element of the wave tile: accumulator (t, mt, r) of lane l is
-// y[m = 16 mt + 4 (l/16) + r, n = 16 (strip0 + t) + l%16].
-__device__ __forceinline__ void store_out(void* out, bool partial, int slot, int M, int N, int m, int n,
-                                          float v) {
-  if (m >= M) return;
-  if (partial)
-    ((float*)out)[((size_t)slot * M + m) * N + n] = v;
-  else
-    ((uint16_t*)out)[(size_t)m * N + n] = f32_to_bf16_bits(v);
-}
+struct GemmArgs {
+  const uint16_t* x;      // bf16 [M, K]
+  const uint8_t* packed;  // strip layout
+  void* out;              // bf16 [M, N] or fp32 [S, M, N]
+  float* ws_part;         // fp32 [S, M, N] workspace (OUT_BF16_VIA_WS)
+  int* ws_cnt;            // one counter per workgroup row range (<= N/16), zero between calls
+  int M, N, K, S, R;      // R = strips per workgroup
+  int mode;
+};
 
-template <int T, int MT, bool F16S, int P>
-__global__ __launch_bounds__(512) void int4_gemm_kernel(const uint16_t* __restrict__ x,
-                                                         const uint4* __restrict__ codes,
-                                                         const uint16_t* __restrict__ scale,
-                                                         const uint16_t* __restrict__ mn,
-                                                         void* __restrict__ out, int M, int N, int K,
-                                                         int S, int partial) {
-  extern __shared__ float red[];
-  const int G = K / kGroup;
+// One accumulator tile element: (mt, lane, r) -> output row m = 16 mt + 4 (lane / 16) + r,
+// column n = 16 strip + lane % 16.
+template <int MT, int GW, bool F16S>
+__global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
+  extern __shared__ float red[];  // [2][W][MT][64][4]
+  const int G = a.K / kGroup;
+  const int nstrips = a.N / 16;
   const int W = blockDim.x >> 6;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
-  const int nrb = N / (16 * T);
-  const int rb = blockIdx.x % nrb;
-  const int slot = blockIdx.x / nrb;
-  const int strip0 = rb * T;
+  const int slot = blockIdx.x % a.S;
+  const int rbi = blockIdx.x / a.S;
+  const int r0 = rbi * a.R;
+  const int r1 = min(nstrips, r0 + a.R);
 
-  const int gs0 = (int)(((long)slot * G) / S), gs1 = (int)(((long)(slot + 1) * G) / S);
-  const int len = gs1 - gs0;
-  const int g0 = gs0 + (wave * len) / W, g1 = gs0 + ((wave + 1) * len) / W;
+  const int nb = (G + GW - 1) / GW;                    // K blocks
+  const int b0 = (int)(((long)slot * nb) / a.S), b1 = (int)(((long)(slot + 1) * nb) / a.S);
+  const int nw = b1 - b0;                              // active waves of this slot
+  const bool active = wave < nw;
+  const int blk = b0 + min(wave, nw - 1);
+  const int gbase = blk * GW;
+  const int ng = min(GW, G - gbase);                   // groups in this block (1..GW)
 
   const uint32_t kExp128 = vgpr_const(0x43004300u);
-  const uint32_t kOnes = 0x3F803F80u;
 
-  f32x4 acc[T][MT];
-#pragma unroll
-  for (int t = 0; t < T; ++t)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Tile pointer of (strip r, group gbase + gw); clamped so that loads past the end re-read a
+  // valid tile (keeps every loop path's load count equal; those values are never used).
+  auto tile_ptr = [&](int r, int gw) {
+    const int rr = min(r, r1 - 1);
+    const int g = gbase + min(gw, ng - 1);
+    return a.packed + ((size_t)rr * G + g) * kTileBytes;
+  };
 
-  Stage<T, MT> st[P];
+  // Two strips of tiles in flight, refilled tile by tile. Issued first: they come from HBM,
+  // the activations below from L2.
+  Tile buf[2][GW];
+  if (active) {
 #pragma unroll
-  for (int p = 0; p < P; ++p)
-    if (g0 + p < g1) load_stage<T, MT>(st[p], codes, scale, mn, x, strip0, G, g0 + p, lane, M, K);
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int gw = 0; gw < GW; ++gw) load_tile(buf[h][gw], tile_ptr(r0 + h, gw), lane);
+  }
 
-  for (int gb = g0; gb < g1; gb += P) {
+  // Activations of this wave's K block, in registers for the whole strip loop.
+  uint4 xa[GW][MT][4];
+  f32x4 X[GW][MT];
+  {
+    const uint32_t kOnes = 0x3F803F80u;
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(kOnes, kOnes, kOnes, kOnes));
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int g = gb + p;
-      if (g < g1) {
-        compute_stage<T, MT, F16S>(st[p], acc, kExp128, kOnes);
-        if (g + P < g1) load_stage<T, MT>(st[p], codes, scale, mn, x, strip0, G, g + P, lane, M, K);
+    for (int gw = 0; gw < GW; ++gw) {
+      const int g = min(gbase + gw, G - 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int xr = min(16 * mt + (lane & 15), a.M - 1);
+        const uint4* p = (const uint4*)(a.x + (size_t)xr * a.K + g * kGroup + 32 * (lane >> 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xa[gw][mt][j] = p[j];
+      }
+    }
+#pragma unroll
+    for (int gw = 0; gw < GW; ++gw)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        X[gw][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          X[gw][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[gw][mt][j]), ones,
+                                                              X[gw][mt], 0, 0, 0);
+      }
+  }
+
+  for (int rb = r0; rb < r1; rb += 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = rb + h;
+      if (r < r1) {
+        f32x4 acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (active) {
+#pragma unroll
+          for (int gw = 0; gw < GW; ++gw) {
+            if (gw < ng) tile_mac<MT, F16S>(buf[h][gw], xa[gw], X[gw], acc, kExp128);
+            load_tile(buf[h][gw], tile_ptr(r + 2, gw), lane);
+          }
+        }
+        // This wave's partial of strip r -> LDS (ring of 2), then the workgroup reduces it.
+        float* mine = red + (((size_t)(r & 1) * W + wave) * MT) * 256;
+        if (active) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) *(f32x4*)(mine + mt * 256 + lane * 4) = acc[mt];
+        }
+        __syncthreads();
+        const float* ring = red + (size_t)(r & 1) * W * MT * 256;
+        for (int e = threadIdx.x; e < MT * 256; e += blockDim.x) {
+          const int mt = e >> 8, l = (e >> 2) & 63, rr = e & 3;
+          const int m = 16 * mt + 4 * (l >> 4) + rr;
+          if (m >= a.M) continue;
+          float v = 0.f;
+          for (int w = 0; w < nw; ++w) v += ring[w * MT * 256 + e];
+          const int n = 16 * r + (l & 15);
+          if (a.mode == OUT_BF16)
+            ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
+          else if (a.mode == OUT_PARTIAL)
+            ((float*)a.out)[((size_t)slot * a.M + m) * a.N + n] = v;
+          else  // agent-scope store: written through to the coherence point, no L2 flush needed
+            __hip_atomic_store(a.ws_part + ((size_t)slot * a.M + m) * a.N + n, v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // The next write to this ring half is two strips later, after the next barrier.
       }
     }
   }
 
-  constexpr int Q = T * MT * 4;  // accumulators per lane
-  if (W == 1) {
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          store_out(out, partial, slot, M, N, 16 * mt + 4 * (lane >> 4) + r, 16 * (strip0 + t) + (lane & 15),
-                    acc[t][mt][r]);
-    return;
-  }
-  // Cross-wave reduction in fixed wave order: red[w][q][lane].
-#pragma unroll
-  for (int t = 0; t < T; ++t)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[(wave * Q + (t * MT + mt) * 4 + r) * 64 + lane] = acc[t][mt][r];
+  if (a.mode != OUT_BF16_VIA_WS) return;
+  // Last-arriving slot of this row range sums the S partials in slot order -> bf16. The
+  // partials were stored at agent scope; waiting for those stores to complete before the
+  // counter increment makes them visible to the last arriver's agent-scope loads, without
+  // the L2 write-back a full __threadfence would cost on every workgroup.
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int e = threadIdx.x; e < Q * 64; e += blockDim.x) {
-    const int q = e >> 6, l = e & 63;
-    float v = red[e];
-    for (int w = 1; w < W; ++w) v += red[w * Q * 64 + e];
-    const int r = q & 3, mt = (q >> 2) % MT, t = (q >> 2) / MT;
-    store_out(out, partial, slot, M, N, 16 * mt + 4 * (l >> 4) + r, 16 * (strip0 + t) + (l & 15), v);
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(a.ws_cnt + rbi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.S - 1;
+  __syncthreads();
+  if (!last) return;
+  const int cols = (r1 - r0) * 16;
+  for (int e = threadIdx.x; e < a.M * cols; e += blockDim.x) {
+    const int m = e / cols, n = r0 * 16 + e % cols;
+    float v = 0.f;
+    for (int s = 0; s < a.S; ++s)
+      v += __hip_atomic_load(a.ws_part + ((size_t)s * a.M + m) * a.N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
   }
+  if (threadIdx.x == 0) __hip_atomic_store(a.ws_cnt + rbi, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------------------- layout kernels
 
 // Engine packing (uint8 [N, K/2], element 2j in the low nibble of byte j; tokenrush/quant.py:9-10)
-// -> strip layout. One thread per output 32-bit word.
-__global__ void pack_kernel(const uint32_t* __restrict__ q, uint32_t* __restrict__ codes, int N, int K) {
+// plus scale/min [N, K/128] -> strip layout. One thread per output 32-bit word (272 per tile).
+__global__ void pack_kernel(const uint32_t* __restrict__ q, const uint16_t* __restrict__ scale,
+                            const uint16_t* __restrict__ mn, uint32_t* __restrict__ packed, int N, int K) {
   const int G = K / kGroup;
-  const size_t total = (size_t)N / 16 * G * 256;
+  const size_t total = (size_t)N / 16 * G * (kTileBytes / 4);
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int j = i & 3, lane = (i >> 2) & 63;
-    const size_t tile = i >> 8;
+    const int d = i % (kTileBytes / 4);
+    const size_t tile = i / (kTileBytes / 4);
     const int g = tile % G;
     const size_t strip = tile / G;
+    if (d >= 256) {
+      const size_t n = strip * 16 + (d - 256);
+      packed[i] = (uint32_t)scale[n * G + g] | ((uint32_t)mn[n * G + g] << 16);
+      continue;
+    }
+    const int j = d & 3, lane = d >> 2;
     const size_t n = strip * 16 + (lane & 15);
     const int k0 = g * kGroup + 32 * (lane >> 4) + 8 * j;
     const uint32_t u = q[(n * K + k0) / 8];  // bytes b0..b3 = codes k0..k0+7
@@ -237,22 +273,30 @@ __global__ void pack_kernel(const uint32_t* __restrict__ q, uint32_t* __restrict
       w |= (b & 0xF) << (4 * p);
       w |= (b >> 4) << (16 + 4 * p);
     }
-    codes[i] = w;
+    packed[i] = w;
   }
 }
 
-// Strip layout -> engine packing (the inverse of pack_kernel).
-__global__ void unpack_kernel(const uint32_t* __restrict__ codes, uint32_t* __restrict__ q, int N, int K) {
+// Strip layout -> engine packing and scale/min (the inverse of pack_kernel).
+__global__ void unpack_kernel(const uint32_t* __restrict__ packed, uint32_t* __restrict__ q,
+                              uint16_t* __restrict__ scale, uint16_t* __restrict__ mn, int N, int K) {
   const int G = K / kGroup;
-  const size_t total = (size_t)N / 16 * G * 256;
+  const size_t total = (size_t)N / 16 * G * (kTileBytes / 4);
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int j = i & 3, lane = (i >> 2) & 63;
-    const size_t tile = i >> 8;
+    const int d = i % (kTileBytes / 4);
+    const size_t tile = i / (kTileBytes / 4);
     const int g = tile % G;
     const size_t strip = tile / G;
+    const uint32_t w = packed[i];
+    if (d >= 256) {
+      const size_t n = strip * 16 + (d - 256);
+      scale[n * G + g] = (uint16_t)(w & 0xFFFF);
+      mn[n * G + g] = (uint16_t)(w >> 16);
+      continue;
+    }
+    const int j = d & 3, lane = d >> 2;
     const size_t n = strip * 16 + (lane & 15);
     const int k0 = g * kGroup + 32 * (lane >> 4) + 8 * j;
-    const uint32_t w = codes[i];
     uint32_t u = 0;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -263,7 +307,7 @@ __global__ void unpack_kernel(const uint32_t* __restrict__ codes, uint32_t* __re
   }
 }
 
-// dequantize_int4 (tokenrush/quant.py:47-53): w = bf16(bf16(q * s) + m), two roundings, from the
+// dequantize_int4 (tokenrush/quant.py:47-53): w = round(round(q * s) + m), two roundings, from the
 // engine packing. One thread per pair of elements (one byte).
 template <bool F16S>
 __global__ void dequant_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ scale,
@@ -304,90 +348,133 @@ using namespace tr;
 
 namespace {
 
-template <int T, int MT, bool F16S>
-hipError_t launch_t(const void* x, const void* codes, const void* scale, const void* mn, void* out, int M,
-                    int N, int K, int S, int W, int partial, hipStream_t stream) {
-  const int nrb = N / (16 * T);
-  const dim3 grid(nrb * S), block(64 * W);
-  const size_t lds = W > 1 ? (size_t)W * T * MT * 4 * 64 * sizeof(float) : 0;
-  hipLaunchKernelGGL((int4_gemm_kernel<T, MT, F16S, 3>), grid, block, lds, stream, (const uint16_t*)x,
-                     (const uint4*)codes, (const uint16_t*)scale, (const uint16_t*)mn, out, M, N, K, S, partial);
+constexpr int kCUs = 256;          // MI355X compute units
+constexpr int kWavesPerCU = 12;    // occupancy of the GEMM kernel (about 150 VGPRs per lane)
+
+struct Plan {
+  int GW, S, W, R, grid_n;
+};
+
+int group_block(int M) { return M > 16 ? 2 : 4; }
+
+// Tiling of an N x K weight for M rows. Depends on M only through the row-tile count
+// (M <= 16 or not), so rows are bit-identical for every M within each range.
+bool make_plan(int N, int K, int M, int S_req, int R_req, Plan* p) {
+  const int G = K / kGroup, nstrips = N / 16;
+  p->GW = group_block(M);
+  const int nb = (G + p->GW - 1) / p->GW;
+  int S = S_req > 0 ? S_req : (nb + kMaxWaves - 1) / kMaxWaves;
+  if (S < 1) S = 1;
+  if (S > nb) return false;
+  const int W = (nb + S - 1) / S;
+  if (W > kMaxWaves) return false;
+  int R = R_req;
+  if (R <= 0) {
+    int wg_per_cu = kWavesPerCU / W;
+    if (wg_per_cu < 1) wg_per_cu = 1;
+    const long slots = (long)kCUs * wg_per_cu;
+    long grid_n = (slots + S - 1) / S;
+    if (grid_n > nstrips) grid_n = nstrips;
+    R = (int)((nstrips + grid_n - 1) / grid_n);
+  }
+  p->S = S;
+  p->W = W;
+  p->R = R;
+  p->grid_n = (nstrips + R - 1) / R;
+  return true;
+}
+
+template <int MT, int GW, bool F16S>
+hipError_t launch_t(const GemmArgs& a, const Plan& p, hipStream_t stream) {
+  const dim3 grid(p.grid_n * p.S), block(64 * p.W);
+  const size_t lds = (size_t)2 * p.W * MT * 256 * sizeof(float);
+  hipLaunchKernelGGL((int4_gemm_kernel<MT, GW, F16S>), grid, block, lds, stream, a);
   return hipGetLastError();
 }
 
-template <bool F16S>
-hipError_t launch_s(int T, int MT, const void* x, const void* codes, const void* scale, const void* mn, void* out,
-                    int M, int N, int K, int S, int W, int partial, hipStream_t stream) {
-#define TR_CASE(TT, MM) \
-  if (T == TT && MT == MM) return launch_t<TT, MM, F16S>(x, codes, scale, mn, out, M, N, K, S, W, partial, stream);
-  TR_CASE(1, 1) TR_CASE(2, 1) TR_CASE(4, 1) TR_CASE(1, 2) TR_CASE(2, 2)
-#undef TR_CASE
-  return hipErrorInvalidValue;
+hipError_t launch(const GemmArgs& a, const Plan& p, int scale_dtype, hipStream_t stream) {
+  const bool f16 = scale_dtype == 1;
+  if (a.M > 16) return f16 ? launch_t<2, 2, true>(a, p, stream) : launch_t<2, 2, false>(a, p, stream);
+  return f16 ? launch_t<1, 4, true>(a, p, stream) : launch_t<1, 4, false>(a, p, stream);
 }
 
 }  // namespace
 
 extern "C" {
 
-// Default tiling for an N x K weight. Independent of M, so every row of the output is
-// computed identically for every M (see the file comment).
-int tr_gemm_plan(int N, int K, int* T, int* W, int* S) {
-  if (N <= 0 || K <= 0 || N % 16 || K % kGroup || !T || !W || !S) return TR_ERR_SHAPE;
-  const int strips = N / 16, G = K / kGroup;
-  int t = 1;
-  if (strips % 2 == 0 && strips / 2 >= 512) t = 2;
-  const int nrb = strips / t;
-  int w = (6144 + nrb - 1) / nrb;     // aim at ~6k waves over the 256 CUs
-  int wmax = G / 3 > 0 ? G / 3 : 1;   // keep >= 3 groups per wave
-  if (w > wmax) w = wmax;
-  if (w > 8) w = 8;
-  if (w < 1) w = 1;
-  *T = t;
-  *W = w;
-  *S = 1;
+int tr_gemm_plan(int N, int K, int M, int* S, int* W, int* R) {
+  if (N <= 0 || K <= 0 || N % 16 || K % kGroup || M < 1 || M > 32 || !S || !W || !R) return TR_ERR_SHAPE;
+  Plan p;
+  if (!make_plan(N, K, M, 0, 0, &p)) return TR_ERR_CONFIG;
+  *S = p.S;
+  *W = p.W;
+  *R = p.R;
   return TR_OK;
 }
 
 int tr_partial_slots(int N, int K, int M) {
-  (void)M;
-  int T, W, S;
-  if (tr_gemm_plan(N, K, &T, &W, &S)) return -1;
+  int S, W, R;
+  if (tr_gemm_plan(N, K, M, &S, &W, &R)) return -1;
   return S;
 }
 
-int tr_int4_gemm_ex(const void* x, const void* packed, const void* scale, const void* mn, void* out,
-                    void* partials, int M, int N, int K, int group, int scale_dtype, int n_slots, int T, int W,
+// Workspace of an out-mode call with S > 1: kWsCounters int32 counters at offset 0 -- a fixed
+// region no call ever uses for partials, so one zero-filled buffer serves calls of every shape
+// -- then the fp32 partials [S, M, N].
+constexpr int kWsCounters = 16384;
+static size_t ws_counter_bytes() { return (size_t)kWsCounters * sizeof(int); }
+
+size_t tr_gemm_workspace_bytes(int N, int K, int M) {
+  Plan p;
+  if (N <= 0 || K <= 0 || N % 16 || K % kGroup || M < 1 || M > 32 || !make_plan(N, K, M, 0, 0, &p)) return 0;
+  if (p.S == 1) return 0;
+  return ws_counter_bytes() + (size_t)p.S * M * N * sizeof(float);
+}
+
+int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials, void* workspace,
+                    size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots, int R,
                     void* stream) {
   if (group != kGroup) return TR_ERR_CONFIG;
   if (M < 0 || M > 32 || N <= 0 || K <= 0 || N % 16 || K % kGroup) return TR_ERR_SHAPE;
   if (M == 0) return TR_OK;
-  if (!x || !packed || !scale || !mn || (!out == !partials)) return TR_ERR_ARG;
+  if (!x || !packed || (!out == !partials)) return TR_ERR_ARG;
   if (scale_dtype != 0 && scale_dtype != 1) return TR_ERR_ARG;
-  if (T != 1 && T != 2 && T != 4) return TR_ERR_CONFIG;
-  if ((N / 16) % T) return TR_ERR_CONFIG;
-  if (T == 4 && M > 16) return TR_ERR_CONFIG;
-  if (W < 1 || W > 8) return TR_ERR_CONFIG;
-  const int partial = partials != nullptr;
-  int S = 1;
-  if (partial) {
-    if (n_slots < 1 || n_slots > K / kGroup) return TR_ERR_CONFIG;
-    S = n_slots;
+  Plan p;
+  if (!make_plan(N, K, M, partials ? n_slots : 0, R, &p)) return TR_ERR_CONFIG;
+  if (partials && p.S != n_slots) return TR_ERR_CONFIG;
+  GemmArgs a;
+  a.x = (const uint16_t*)x;
+  a.packed = (const uint8_t*)packed;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.S = p.S;
+  a.R = p.R;
+  a.ws_part = nullptr;
+  a.ws_cnt = nullptr;
+  if (partials) {
+    a.mode = OUT_PARTIAL;
+    a.out = partials;
+  } else if (p.S == 1) {
+    a.mode = OUT_BF16;
+    a.out = out;
+  } else {
+    const size_t need = ws_counter_bytes() + (size_t)p.S * M * N * sizeof(float);
+    if (!workspace || workspace_bytes < need) return TR_ERR_ARG;
+    if (p.grid_n > kWsCounters) return TR_ERR_CONFIG;
+    a.mode = OUT_BF16_VIA_WS;
+    a.out = out;
+    a.ws_cnt = (int*)workspace;
+    a.ws_part = (float*)((char*)workspace + ws_counter_bytes());
   }
-  const int MT = M > 16 ? 2 : 1;
-  hipError_t e = scale_dtype == 1
-                     ? launch_s<true>(T, MT, x, packed, scale, mn, partial ? partials : out, M, N, K, S, W, partial,
-                                      (hipStream_t)stream)
-                     : launch_s<false>(T, MT, x, packed, scale, mn, partial ? partials : out, M, N, K, S, W,
-                                       partial, (hipStream_t)stream);
-  return e == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+  return launch(a, p, scale_dtype, (hipStream_t)stream) == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
-int tr_int4_gemm(const void* x, const void* packed, const void* scale, const void* mn, void* out, void* partials,
-                 int M, int N, int K, int group, int scale_dtype, int n_slots, void* stream) {
-  int T, W, S;
-  int rc = tr_gemm_plan(N, K, &T, &W, &S);
-  if (rc) return rc;
-  return tr_int4_gemm_ex(x, packed, scale, mn, out, partials, M, N, K, group, scale_dtype, n_slots, T, W, stream);
+int tr_int4_gemm(const void* x, const void* packed, void* out, void* partials, void* workspace,
+                 size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
+                 void* stream) {
+  return tr_int4_gemm_ex(x, packed, out, partials, workspace, workspace_bytes, M, N, K, group, scale_dtype,
+                         n_slots, 0, stream);
 }
 
 static int grid_for(size_t work) {
@@ -397,21 +484,21 @@ static int grid_for(size_t work) {
   return (int)b;
 }
 
-int tr_pack_int4(const void* qweight, void* packed, int N, int K, void* stream) {
-  if (!qweight || !packed) return TR_ERR_ARG;
+int tr_pack_int4(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K, void* stream) {
+  if (!qweight || !scale || !mn || !packed) return TR_ERR_ARG;
   if (N <= 0 || K <= 0 || N % 16 || K % kGroup) return TR_ERR_SHAPE;
-  const size_t total = (size_t)N / 16 * (K / kGroup) * 256;
+  const size_t total = (size_t)N / 16 * (K / kGroup) * (kTileBytes / 4);
   hipLaunchKernelGGL(pack_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, (const uint32_t*)qweight,
-                     (uint32_t*)packed, N, K);
+                     (const uint16_t*)scale, (const uint16_t*)mn, (uint32_t*)packed, N, K);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
-int tr_unpack_int4(const void* packed, void* qweight, int N, int K, void* stream) {
-  if (!qweight || !packed) return TR_ERR_ARG;
+int tr_unpack_int4(const void* packed, void* qweight, void* scale, void* mn, int N, int K, void* stream) {
+  if (!qweight || !packed || !scale || !mn) return TR_ERR_ARG;
   if (N <= 0 || K <= 0 || N % 16 || K % kGroup) return TR_ERR_SHAPE;
-  const size_t total = (size_t)N / 16 * (K / kGroup) * 256;
+  const size_t total = (size_t)N / 16 * (K / kGroup) * (kTileBytes / 4);
   hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint32_t*)packed, (uint32_t*)qweight, N, K);
+                     (const uint32_t*)packed, (uint32_t*)qweight, (uint16_t*)scale, (uint16_t*)mn, N, K);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 

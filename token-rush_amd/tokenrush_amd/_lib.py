@@ -21,13 +21,15 @@ _ERRORS = {ERR_SHAPE: "problem shape not supported", ERR_CONFIG: "no kernel conf
 
 _P, _I = ctypes.c_void_p, ctypes.c_int
 # name -> (restype, argtypes); the signatures of include/tokenrush_hip.h
+_S = ctypes.c_size_t
 SIGNATURES = {
-    "tr_gemm_plan": (_I, [_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "tr_gemm_plan": (_I, [_I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "tr_partial_slots": (_I, [_I, _I, _I]),
-    "tr_int4_gemm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
-    "tr_int4_gemm_ex": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
-    "tr_pack_int4": (_I, [_P, _P, _I, _I, _P]),
-    "tr_unpack_int4": (_I, [_P, _P, _I, _I, _P]),
+    "tr_gemm_workspace_bytes": (_S, [_I, _I, _I]),
+    "tr_int4_gemm": (_I, [_P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _I, _P]),
+    "tr_int4_gemm_ex": (_I, [_P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "tr_pack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "tr_unpack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "tr_dequant_int4": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
 }
 

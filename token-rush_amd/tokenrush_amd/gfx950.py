@@ -1,16 +1,19 @@
 """Strip-layout int4 GEMM for M <= 32 rows on MI355X (gfx950).
 
 This module plays the role of the reference's tokenrush/marlin.py (marlin.py:1-168): it
-converts the engine's packing to the kernel's weight layout and back, and launches the
-kernel. The kernel itself (csrc/int4_gemm.hip) is our own design, not Marlin:
+converts the engine's packing to the kernel's weight layout and back, sizes the workspace
+before graph capture, and launches the kernel. The kernel (csrc/int4_gemm.hip) is our own
+design, not Marlin:
 
-* weight layout: codes [N/16, K/128, 64, 16] uint8 -- one 1 KiB tile per (16-row strip,
-  group of 128), in the order one wave's 16-byte loads consume it; scale and min stay in the
-  engine's [N, K/128] layout;
-* every M in 1..32 runs the same MFMA instructions (rows beyond M are zero lanes), so each
+* weight layout: uint8 [N/16, K/128, 1088] -- one tile per (16-row strip, group of 128):
+  1 KiB of codes in the order one wave's 16-byte loads consume them, then the 16 rows'
+  (scale, min) pairs, so a strip is one contiguous stream;
+* every M in 1..16 runs the same instructions (rows beyond M are padding lanes), so each
   output row is bit-identical for every M, as Marlin's is (reference test_marlin.py:42-52);
-* no locks and no reduce buffer: split-K happens inside a workgroup and is reduced through
-  LDS in a fixed order; mul_partial writes fp32 slots [S, M, N] whose sum is the product.
+  the same holds within M = 17..32;
+* no locks: split-K inside a workgroup is reduced through LDS in a fixed order; split-K
+  across workgroups (K = 17408, or M > 16) writes fp32 slots, which mul_partial returns as
+  [S, M, N] and mul reduces in the last-arriving workgroup through the workspace.
 
 API (same names and argument meaning as marlin.py): ext, available, pack, unpack,
 workspaces, mul, partial_slots, mul_partial.
@@ -22,7 +25,8 @@ import torch
 from . import _lib
 
 GROUP = 128
-MAX_ROWS = 32        # the kernel's row limit (two 16-row MFMA tiles)
+TILE = 1088
+MAX_ROWS = 32        # two 16-row MFMA tiles
 SCALE_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 
@@ -42,100 +46,136 @@ def available() -> bool:
 
 
 def _check_shape(N: int, K: int):
-    if N % 16 or K % GROUP:
+    if N % 16 or K % GROUP or N <= 0 or K <= 0:
         raise RuntimeError(f"problem shape (n={N}, k={K}) not supported: need n % 16 == 0, k % {GROUP} == 0")
 
 
+def _sm_views(B: torch.Tensor, dtype):
+    """(scale, min) as strided views [N/16, K/128, 16] into the tiles of B."""
+    sm = B[..., 1024:].view(dtype).unflatten(-1, (16, 2))
+    return sm[..., 0], sm[..., 1]
+
+
 def pack(qweight: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor):
-    """Engine packing (uint8 [N, K/2], bf16/fp16 [N, K/128] x2) -> strip layout
-    (uint8 [N/16, K/128, 64, 16], scale, mn). The counterpart of marlin.pack (marlin.py:73-96)."""
+    """Engine packing (uint8 [N, K/2], bf16/fp16 [N, K/128] x2) -> (B, s, m): B is the strip
+    layout uint8 [N/16, K/128, 1088] holding codes, scale and min; s and m are views into B
+    (they carry the scale dtype). The counterpart of marlin.pack (marlin.py:73-96)."""
     _lib.require_gpu(qweight, scale, mn)
     N, K = qweight.shape[0], qweight.shape[1] * 2
     _check_shape(N, K)
-    assert qweight.dtype == torch.uint8 and scale.shape == mn.shape == (N, K // GROUP), (scale.shape, N, K)
-    q = qweight.contiguous()
-    B = torch.empty(N // 16, K // GROUP, 64, 16, dtype=torch.uint8, device=q.device)
-    _lib.check(ext().tr_pack_int4(_lib.ptr(q), _lib.ptr(B), N, K, _lib.stream_of(q)), "tr_pack_int4")
-    return B, scale.contiguous(), mn.contiguous()
+    if qweight.dtype != torch.uint8 or scale.shape != (N, K // GROUP) or mn.shape != scale.shape:
+        raise RuntimeError(f"expected uint8 [N, K/2] and [N, K/{GROUP}] scale/min, got {scale.shape}")
+    if scale.dtype not in SCALE_DTYPES or mn.dtype != scale.dtype:
+        raise RuntimeError("scale/min must both be bf16 or fp16")
+    q, s, m = qweight.contiguous(), scale.contiguous(), mn.contiguous()
+    B = torch.empty(N // 16, K // GROUP, TILE, dtype=torch.uint8, device=q.device)
+    _lib.check(ext().tr_pack_int4(_lib.ptr(q), _lib.ptr(s), _lib.ptr(m), _lib.ptr(B), N, K, _lib.stream_of(q)),
+               "tr_pack_int4")
+    return (B,) + _sm_views(B, scale.dtype)
 
 
 def unpack(B: torch.Tensor, s: torch.Tensor, m: torch.Tensor):
-    """Inverse of pack -> (qweight uint8 [N, K/2], scale, mn) (marlin.unpack, marlin.py:99-118)."""
-    _lib.require_gpu(B, s, m)
+    """Inverse of pack -> (qweight uint8 [N, K/2], scale [N, K/128], mn [N, K/128])
+    (marlin.unpack, marlin.py:99-118). s only supplies the scale dtype."""
+    _lib.require_gpu(B)
     N, K = B.shape[0] * 16, B.shape[1] * GROUP
     q = torch.empty(N, K // 2, dtype=torch.uint8, device=B.device)
-    _lib.check(ext().tr_unpack_int4(_lib.ptr(B), _lib.ptr(q), N, K, _lib.stream_of(B)), "tr_unpack_int4")
-    return q, s.contiguous(), m.contiguous()
+    sc = torch.empty(N, K // GROUP, dtype=s.dtype, device=B.device)
+    mn = torch.empty_like(sc)
+    _lib.check(ext().tr_unpack_int4(_lib.ptr(B), _lib.ptr(q), _lib.ptr(sc), _lib.ptr(mn), N, K, _lib.stream_of(B)),
+               "tr_unpack_int4")
+    return q, sc, mn
 
 
-def workspaces(N: int, device):
-    """Kept for API parity with marlin.workspaces (marlin.py:121-135): this kernel needs no
-    lock array and no reduce buffer, so there is nothing to size before graph capture."""
-    return None, None
+_ws = {}
 
 
-def plan(N: int, K: int):
-    """(T, W, S): strips per workgroup, waves per workgroup, K slots. Depends on (N, K) only."""
-    T, W, S = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    _lib.check(ext().tr_gemm_plan(N, K, ctypes.byref(T), ctypes.byref(W), ctypes.byref(S)), "tr_gemm_plan")
-    return T.value, W.value, S.value
+def workspace_bytes(N: int, K: int, M: int = MAX_ROWS) -> int:
+    return int(ext().tr_gemm_workspace_bytes(N, K, M))
 
 
-def _launch(x, B, s, m, y, partial, n_slots, thread_t, thread_w):
+def workspaces(N: int, device, K: int = None, M: int = MAX_ROWS):
+    """The per-device workspace of mul(), grown to fit an N x K weight at up to M rows
+    (marlin.workspaces, marlin.py:121-135: grow before graph capture; QLinear does so at
+    construction). Zero-filled: its counters must read zero between calls, which every call
+    restores. Calls that overlap on one device (different streams) would share it."""
+    key = torch.device(device).index or 0
+    ws = _ws.get(key)
+    need = 0
+    if K is not None:
+        need = max(workspace_bytes(N, K, mm) for mm in {1, min(M, 16), M})
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
+        _ws[key] = ws
+    return ws, ws.numel()
+
+
+def plan(N: int, K: int, M: int = 1):
+    """(S, W, R): K slots, waves per workgroup, strips per workgroup. Depends on M only
+    through M > 16."""
+    S, W, R = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.check(ext().tr_gemm_plan(N, K, M, ctypes.byref(S), ctypes.byref(W), ctypes.byref(R)), "tr_gemm_plan")
+    return S.value, W.value, R.value
+
+
+def _launch(x, B, s, y, partial, n_slots, strips_per_wg=-1):
     M, K = x.shape
     N = B.shape[0] * 16
-    if x.dtype != torch.bfloat16 or s.dtype not in SCALE_DTYPES or m.dtype != s.dtype:
+    if x.dtype != torch.bfloat16 or s.dtype not in SCALE_DTYPES:
         raise RuntimeError("dtypes: x must be bf16, scale/min bf16 or fp16")
-    if not (x.is_contiguous() and B.is_contiguous() and s.is_contiguous() and m.is_contiguous()):
+    if not (x.is_contiguous() and B.is_contiguous()):
         raise RuntimeError("inputs must be contiguous")
-    if M > MAX_ROWS or K != B.shape[1] * GROUP:
+    if M > MAX_ROWS or K != B.shape[1] * GROUP or B.shape[2] != TILE:
         raise RuntimeError(f"problem shape (m={M}, n={N}, k={K}) not supported: need m <= {MAX_ROWS}")
-    _lib.require_gpu(x, B, s, m, y)
-    st = _lib.stream_of(x)
+    _lib.require_gpu(x, B, y)
+    ws, nbytes = None, 0
+    if not partial and workspace_bytes(N, K, M) > 0:
+        ws, nbytes = workspaces(N, x.device, K, M)
+        if nbytes < workspace_bytes(N, K, M):
+            raise RuntimeError("workspace too small: call workspaces(N, device, K) before graph capture")
     out, part = (None, y) if partial else (y, None)
-    if thread_t == -1 and thread_w == -1:
-        rc = ext().tr_int4_gemm(_lib.ptr(x), _lib.ptr(B), _lib.ptr(s), _lib.ptr(m), _lib.ptr(out), _lib.ptr(part),
-                                M, N, K, GROUP, SCALE_DTYPES[s.dtype], n_slots, st)
+    args = (_lib.ptr(x), _lib.ptr(B), _lib.ptr(out), _lib.ptr(part), _lib.ptr(ws), nbytes, M, N, K, GROUP,
+            SCALE_DTYPES[s.dtype], n_slots)
+    st = _lib.stream_of(x)
+    if strips_per_wg == -1:
+        rc = ext().tr_int4_gemm(*args, st)
     else:
-        T0, W0, _ = plan(N, K)
-        T = T0 if thread_t == -1 else thread_t
-        W = W0 if thread_w == -1 else thread_w
-        rc = ext().tr_int4_gemm_ex(_lib.ptr(x), _lib.ptr(B), _lib.ptr(s), _lib.ptr(m), _lib.ptr(out), _lib.ptr(part),
-                                   M, N, K, GROUP, SCALE_DTYPES[s.dtype], n_slots, T, W, st)
+        rc = ext().tr_int4_gemm_ex(*args, strips_per_wg, st)
     _lib.check(rc, f"tr_int4_gemm (m={M}, n={N}, k={K})")
 
 
-def mul(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor, thread_t=-1, thread_w=-1):
-    """x [M, K] bf16 (M <= 32) -> [M, N] bf16 (marlin.mul, marlin.py:138-145)."""
-    M = x.shape[0]
-    y = torch.empty(M, B.shape[0] * 16, dtype=torch.bfloat16, device=x.device)
-    _launch(x, B, s, m, y, False, 0, thread_t, thread_w)
+def mul(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor = None, strips_per_wg=-1):
+    """x [M, K] bf16 (M <= 32) -> [M, N] bf16 (marlin.mul, marlin.py:138-145).
+    s (from pack) supplies the scale dtype; m is accepted for call compatibility."""
+    y = torch.empty(x.shape[0], B.shape[0] * 16, dtype=torch.bfloat16, device=x.device)
+    _launch(x, B, s, y, False, 0, strips_per_wg)
     return y
 
 
 _slots = {}
 
 
-def partial_slots(N: int, K: int) -> int:
-    """fp32 slots mul_partial writes for an N x K weight (marlin.partial_slots, marlin.py:151-155)."""
-    key = (N, K)
+def partial_slots(N: int, K: int, M: int = 1) -> int:
+    """fp32 slots mul_partial writes for an N x K weight at M rows
+    (marlin.partial_slots, marlin.py:151-155)."""
+    key = (N, K, M > 16)
     if key not in _slots:
-        S = ext().tr_partial_slots(N, K, 1)
+        S = ext().tr_partial_slots(N, K, M)
         if S < 1:
             raise RuntimeError(f"problem shape (n={N}, k={K}) not supported")
         _slots[key] = S
     return _slots[key]
 
 
-def mul_partial(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor, n_slots: int = None,
-                thread_t=-1, thread_w=-1):
+def mul_partial(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor = None, n_slots: int = None,
+                strips_per_wg=-1):
     """x [M, K] bf16 (M <= 32) -> fp32 partials [S, M, N] whose sum over S is the product
     (marlin.mul_partial, marlin.py:158-168). Every slot is written."""
     M, K = x.shape
     N = B.shape[0] * 16
-    S = partial_slots(N, K) if n_slots is None else n_slots
+    S = partial_slots(N, K, M) if n_slots is None else n_slots
     y = torch.empty(S, M, N, dtype=torch.float32, device=x.device)
-    _launch(x, B, s, m, y, True, S, thread_t, thread_w)
+    _launch(x, B, s, y, True, S, strips_per_wg)
     return y
 
 

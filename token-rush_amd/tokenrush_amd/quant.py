@@ -69,6 +69,7 @@ class QLinear:
             if self.group != GROUP:
                 raise RuntimeError(f"gfx950 backend needs group {GROUP}, got {self.group}")
             self.B, self.s, self.m = gfx950.pack(qweight, scale, mn)
+            gfx950.workspaces(self.shape_[0], qweight.device, self.shape_[1])   # sized before any graph capture
             self.qweight = self.scale = self.mn = None
         else:
             self.qweight, self.scale, self.mn = qweight, scale, mn
@@ -86,7 +87,7 @@ class QLinear:
 
     @property
     def nbytes(self):
-        ts = (self.B, self.s, self.m) if self.backend == "gfx950" else (self.qweight, self.scale, self.mn)
+        ts = (self.B,) if self.backend == "gfx950" else (self.qweight, self.scale, self.mn)
         return sum(t.numel() * t.element_size() for t in ts)
 
     def nibbles(self):
@@ -106,11 +107,11 @@ class QLinear:
         T = x.shape[0]
         if self.backend == "dequant" or T > MAX_ROWS:
             return F.linear(x, self.dequantize().to(x.dtype))
-        return gfx950.mul(x.contiguous(), self.B, self.s, self.m)
+        return gfx950.mul(x.contiguous(), self.B, self.s)
 
     def partials(self, x: torch.Tensor) -> torch.Tensor:
         """x [T, K] -> [S, T, N] fp32 whose sum over S is the product (S == 1 unless split-K)."""
         T = x.shape[0]
         if self.backend == "gfx950" and self.split_k > 1 and T <= MAX_ROWS:
-            return gfx950.mul_partial(x.contiguous(), self.B, self.s, self.m)
+            return gfx950.mul_partial(x.contiguous(), self.B, self.s)
         return self(x).float()[None]
