@@ -43,8 +43,10 @@ int tr_int4_gemm(const void* x, const void* packed, void* out, void* partials, v
                  size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
                  void* stream);
 
-/* tr_int4_gemm with an explicit number of 16-row strips per workgroup (R > 0; R <= 0 = default).
- * The role of Marlin's thread_k/thread_n/sms overrides (tokenrush/csrc/marlin_bf16.cpp:14-16). */
+/* tr_int4_gemm with an explicit tiling: n_slots K slots (also in out mode; 0 = default) and R
+ * 16-row strips per workgroup (R <= 0 = default). The workspace must then fit that S (sizing as
+ * tr_gemm_workspace_bytes does, with S slots). The role of Marlin's thread_k/thread_n/sms
+ * overrides (tokenrush/csrc/marlin_bf16.cpp:14-16). */
 int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials, void* workspace,
                     size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
                     int R, void* stream);

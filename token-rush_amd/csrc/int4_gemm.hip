@@ -139,22 +139,10 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     return a.packed + ((size_t)rr * G + g) * kTileBytes;
   };
 
-  // Two strips of tiles in flight, refilled tile by tile. Issued first: they come from HBM,
-  // the activations below from L2.
-  Tile buf[2][GW];
-  if (active) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int gw = 0; gw < GW; ++gw) load_tile(buf[h][gw], tile_ptr(r0 + h, gw), lane);
-  }
-
   // Activations of this wave's K block, in registers for the whole strip loop.
   uint4 xa[GW][MT][4];
   f32x4 X[GW][MT];
   {
-    const uint32_t kOnes = 0x3F803F80u;
-    const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(kOnes, kOnes, kOnes, kOnes));
 #pragma unroll
     for (int gw = 0; gw < GW; ++gw) {
       const int g = min(gbase + gw, G - 1);
@@ -166,6 +154,21 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
         for (int j = 0; j < 4; ++j) xa[gw][mt][j] = p[j];
       }
     }
+  }
+  // Two strips of tiles in flight, refilled tile by tile. Issued after the activation loads:
+  // vmcnt counts loads in issue order, so the ones-MFMA below waits only for the (L2-resident)
+  // activations and each tile_mac only for its own tile.
+  Tile buf[2][GW];
+  if (active) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int gw = 0; gw < GW; ++gw) load_tile(buf[h][gw], tile_ptr(r0 + h, gw), lane);
+  }
+
+  {
+    const uint32_t kOnes = 0x3F803F80u;
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(kOnes, kOnes, kOnes, kOnes));
 #pragma unroll
     for (int gw = 0; gw < GW; ++gw)
 #pragma unroll
@@ -440,7 +443,7 @@ int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials
   if (!x || !packed || (!out == !partials)) return TR_ERR_ARG;
   if (scale_dtype != 0 && scale_dtype != 1) return TR_ERR_ARG;
   Plan p;
-  if (!make_plan(N, K, M, partials ? n_slots : 0, R, &p)) return TR_ERR_CONFIG;
+  if (!make_plan(N, K, M, n_slots, R, &p)) return TR_ERR_CONFIG;
   if (partials && p.S != n_slots) return TR_ERR_CONFIG;
   GemmArgs a;
   a.x = (const uint16_t*)x;
@@ -474,7 +477,7 @@ int tr_int4_gemm(const void* x, const void* packed, void* out, void* partials, v
                  size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
                  void* stream) {
   return tr_int4_gemm_ex(x, packed, out, partials, workspace, workspace_bytes, M, N, K, group, scale_dtype,
-                         n_slots, 0, stream);
+                         partials ? n_slots : 0, 0, stream);
 }
 
 static int grid_for(size_t work) {

@@ -94,16 +94,16 @@ def workspace_bytes(N: int, K: int, M: int = MAX_ROWS) -> int:
     return int(ext().tr_gemm_workspace_bytes(N, K, M))
 
 
-def workspaces(N: int, device, K: int = None, M: int = MAX_ROWS):
+def workspaces(N: int, device, K: int = None, M: int = MAX_ROWS, min_bytes: int = 0):
     """The per-device workspace of mul(), grown to fit an N x K weight at up to M rows
     (marlin.workspaces, marlin.py:121-135: grow before graph capture; QLinear does so at
     construction). Zero-filled: its counters must read zero between calls, which every call
     restores. Calls that overlap on one device (different streams) would share it."""
     key = torch.device(device).index or 0
     ws = _ws.get(key)
-    need = 0
+    need = min_bytes
     if K is not None:
-        need = max(workspace_bytes(N, K, mm) for mm in {1, min(M, 16), M})
+        need = max([need] + [workspace_bytes(N, K, mm) for mm in {1, min(M, 16), M}])
     if ws is None or ws.numel() < need:
         ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
         _ws[key] = ws
@@ -118,7 +118,7 @@ def plan(N: int, K: int, M: int = 1):
     return S.value, W.value, R.value
 
 
-def _launch(x, B, s, y, partial, n_slots, strips_per_wg=-1):
+def _launch(x, B, s, y, partial, n_slots, strips_per_wg=-1, slots=0):
     M, K = x.shape
     N = B.shape[0] * 16
     if x.dtype != torch.bfloat16 or s.dtype not in SCALE_DTYPES:
@@ -129,26 +129,30 @@ def _launch(x, B, s, y, partial, n_slots, strips_per_wg=-1):
         raise RuntimeError(f"problem shape (m={M}, n={N}, k={K}) not supported: need m <= {MAX_ROWS}")
     _lib.require_gpu(x, B, y)
     ws, nbytes = None, 0
-    if not partial and workspace_bytes(N, K, M) > 0:
-        ws, nbytes = workspaces(N, x.device, K, M)
-        if nbytes < workspace_bytes(N, K, M):
+    need = workspace_bytes(N, K, M) if slots == 0 else (65536 + 4 * slots * M * N if slots > 1 else 0)
+    if not partial and need > 0:
+        ws, nbytes = workspaces(N, x.device, K, M, min_bytes=need)
+        if nbytes < need:
             raise RuntimeError("workspace too small: call workspaces(N, device, K) before graph capture")
     out, part = (None, y) if partial else (y, None)
     args = (_lib.ptr(x), _lib.ptr(B), _lib.ptr(out), _lib.ptr(part), _lib.ptr(ws), nbytes, M, N, K, GROUP,
             SCALE_DTYPES[s.dtype], n_slots)
     st = _lib.stream_of(x)
-    if strips_per_wg == -1:
+    if strips_per_wg == -1 and slots == 0:
         rc = ext().tr_int4_gemm(*args, st)
     else:
+        if not partial:
+            args = args[:-1] + (slots,)
         rc = ext().tr_int4_gemm_ex(*args, strips_per_wg, st)
     _lib.check(rc, f"tr_int4_gemm (m={M}, n={N}, k={K})")
 
 
-def mul(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor = None, strips_per_wg=-1):
+def mul(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor = None, strips_per_wg=-1, slots=0):
     """x [M, K] bf16 (M <= 32) -> [M, N] bf16 (marlin.mul, marlin.py:138-145).
-    s (from pack) supplies the scale dtype; m is accepted for call compatibility."""
+    s (from pack) supplies the scale dtype; m is accepted for call compatibility.
+    strips_per_wg / slots override the tiling (0 / -1 = default)."""
     y = torch.empty(x.shape[0], B.shape[0] * 16, dtype=torch.bfloat16, device=x.device)
-    _launch(x, B, s, y, False, 0, strips_per_wg)
+    _launch(x, B, s, y, False, 0, strips_per_wg, slots)
     return y
 
 
