@@ -20,6 +20,7 @@
 #define TOKENRUSH_HIP_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -74,6 +75,66 @@ int tr_unpack_int4(const void* packed, void* qweight, void* scale, void* mn, int
  * Replaces: dequantize_int4 (tokenrush/quant.py:47-53). */
 int tr_dequant_int4(const void* qweight, const void* scale, const void* mn, void* out, int N, int K,
                     int group, int scale_dtype, void* stream);
+
+/* ---------------------------------------------------------------- verify accept / commit
+ *
+ * logits bf16 [M, V] (1 <= M <= 32, 64 <= V <= 262144); tokens int64. `ws` is the accept
+ * workspace (tr_accept_workspace_bytes(M, V) bytes, zero-filled before first use; every call
+ * leaves its counters at zero again; calls that overlap on one device must not share it).
+ * Outputs (device int64): pred [M] (target token per row; may be null), n_accepted [1], tok [1]
+ * (correction or bonus token), pos [1] (device position, advanced in place by n + 1), slot [1]
+ * (recurrent-state slot to keep), tokens [M] (accepted drafts then tok, -1 beyond), commit [M]
+ * (chains: positions pos..pos+n; trees: node indices root..best; -1 beyond).
+ * Each call is one launch (residual: three) with no host synchronization. */
+
+size_t tr_accept_workspace_bytes(int M, int V);
+
+/* Per-row argmax, first index on ties. Replaces: logits.argmax(-1) (tokenrush/sample.py:37-38). */
+int tr_argmax_rows(const void* logits, int M, int V, void* ws, size_t ws_bytes, int64_t* pred, void* stream);
+
+/* Greedy verify: pred = argmax, n = leading matches of pred[:M-1] with spec_toks[1:M],
+ * tok = pred[n], pos += n + 1, slot = n.
+ * Replaces: Engine._verify_step's accept with temperature 0 (tokenrush/model.py:302-312). */
+int tr_accept_greedy(const void* logits, int M, int V, const int64_t* spec_toks, void* ws, size_t ws_bytes,
+                     int64_t* pred, int64_t* n_accepted, int64_t* tok, int64_t* pos, int64_t* slot,
+                     int64_t* tokens, int64_t* commit, void* stream);
+
+/* sample(): top-64 per row (value desc, index asc), temperature / top_p / top_k masked softmax,
+ * inverse-CDF pick with u [M]; greedy when *temperature == 0. Parameters are device scalars.
+ * Replaces: sample(logits, params, u) (tokenrush/sample.py:30-51). */
+int tr_sample(const void* logits, int M, int V, const float* temperature, const float* top_p,
+              const int64_t* top_k, const float* u, void* ws, size_t ws_bytes, int64_t* out, void* stream);
+
+/* Sampled verify: pred = sample(...), then the leading-match commit of tr_accept_greedy.
+ * Replaces: Engine._verify_step (tokenrush/model.py:302-312) with SamplingParams. */
+int tr_accept_sample(const void* logits, int M, int V, const int64_t* spec_toks, const float* temperature,
+                     const float* top_p, const int64_t* top_k, const float* u, void* ws, size_t ws_bytes,
+                     int64_t* pred, int64_t* n_accepted, int64_t* tok, int64_t* pos, int64_t* slot,
+                     int64_t* tokens, int64_t* commit, void* stream);
+
+/* Speculative sampling with residual resample (Leviathan et al. 2023): q fp32 [M-1, V] draft
+ * probabilities, u fp32 [M]. Draft i accepted when u[i] q[i, d_i] < p[i, d_i] (p = softmax of
+ * row i); at the first rejection j (or j = M-1) tok is drawn with u[M-1] from max(p_j - q_j, 0)
+ * (p_{M-1} when all pass). No counterpart in the reference (its sampled verify is
+ * tr_accept_sample's rule, tokenrush/model.py:302-308; progress.md:649-656). */
+int tr_accept_residual(const void* logits, int M, int V, const float* q, const int64_t* spec_toks,
+                       const float* u, void* ws, size_t ws_bytes, int64_t* n_accepted, int64_t* tok,
+                       int64_t* pos, int64_t* slot, int64_t* tokens, int64_t* commit, void* stream);
+
+/* Draft-tree verify: node 0 is the root (parent -1), parent[i] < i; node i accepted when
+ * node_toks[i] == argmax(row parent[i]) and its parent is accepted; the deepest accepted node
+ * (lowest index among equals) ends the path. slot = that node, commit = path node indices.
+ * Replaces: the host tree simulation of bench/tree_accept.py:91-100. */
+int tr_accept_tree(const void* logits, int M, int V, const int64_t* node_toks, const int32_t* parent, void* ws,
+                   size_t ws_bytes, int64_t* pred, int64_t* n_accepted, int64_t* tok, int64_t* pos,
+                   int64_t* slot, int64_t* tokens, int64_t* commit, void* stream);
+
+/* Tree commit of a cache laid out [planes][max_len][row_bytes]: row (pos - n - 1) + commit[t]
+ * moves to row (pos - n - 1) + t for t = 1..n, reading n and pos after the accept. For the
+ * reference's KV cache and its scales (tokenrush/state.py:19-29), whose chain commit is only
+ * the position advance (model.py:376-382). */
+int tr_commit_rows(void* data, int planes, long plane_stride_bytes, int row_bytes, const int64_t* pos,
+                   const int64_t* n_accepted, const int64_t* commit, int max_n, void* stream);
 
 #ifdef __cplusplus
 }

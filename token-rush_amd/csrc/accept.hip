@@ -1,0 +1,869 @@
+// On-device accept/commit of the speculative verify step, for gfx950.
+//
+// Every kernel splits each vocabulary row into chunks handled by separate workgroups and
+// finishes with "last arriver" reductions: each workgroup publishes its partial result to the
+// caller's workspace with agent-scope stores, then increments a per-row counter; the workgroup
+// that brings the counter to its total reduces the row (and, one level up, the last row
+// finishes the accept). Counters are reset by the workgroup that consumes them, so a zero-filled
+// workspace stays valid across calls and graph replays, and one launch does the whole job.
+//
+// Arithmetic is fixed so that the CPU oracle (oracle/accept.py) reproduces it bit for bit:
+//   * texp(): Cody-Waite reduction with ln2 split hi/lo, degree-7 Taylor polynomial of e^r in
+//     Horner form, 2^n through the exponent field; x < -80 -> 0. Constants are fp32 bit
+//     patterns. The file is compiled with -ffp-contract=off and uses explicitly rounded
+//     operations, so every step is one fp32 rounding.
+//   * sums over the 64 sampling candidates are sequential in rank order;
+//   * sums over a vocabulary row are blocked: sequential over runs of 16 elements, over the 64
+//     runs of a 1024-element chunk, then over chunks.
+//   * ties: argmax takes the first index; the top-64 candidates are ordered by value
+//     descending, then index ascending.
+// Logits are bf16; NaN logits are not supported.
+#include "tr_common.h"
+
+namespace tr {
+
+// ------------------------------------------------------------------ shared helpers
+
+constexpr int kCand = 64;          // sampling candidates (tokenrush/sample.py:12)
+constexpr int kTopChunk = 4096;    // elements per workgroup in the argmax / top-64 kernels
+constexpr int kRun = 16, kChunk = 1024;
+
+template <typename T>
+__device__ __forceinline__ void ws_st(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T ws_ld(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// True (in every thread) for the workgroup that completes `total` arrivals at *cnt; that
+// workgroup also resets the counter. Agent-scope stores made before the call are visible to
+// the last arriver's agent-scope loads.
+__device__ __forceinline__ bool arrive_last(int* cnt, int total) {
+  __shared__ int flag;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flag = old == total - 1;
+    if (flag) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  return flag;
+}
+
+// bf16 bits -> unsigned key increasing with the value.
+__device__ __forceinline__ uint32_t ord16(uint32_t b) { return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u); }
+__device__ __forceinline__ uint32_t unord16(uint32_t k) { return (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu); }
+// (value, index) -> one 64-bit key: larger value first, then smaller index.
+__device__ __forceinline__ uint64_t vkey(uint32_t k16, uint32_t idx) {
+  return ((uint64_t)k16 << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+__device__ __forceinline__ uint32_t vkey_idx(uint64_t k) { return 0xFFFFFFFFu - (uint32_t)k; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t w = __shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// Block-wide exclusive prefix sum of one int per thread (blockDim.x <= 1024), plus the total.
+__device__ int block_exclusive_scan(int v, int* total) {
+  __shared__ int wsum[16];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wid] = x;
+  __syncthreads();
+  int base = 0, tot = 0;
+  for (int w = 0; w < nw; ++w) {
+    if (w < wid) base += wsum[w];
+    tot += wsum[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return base + x - v;
+}
+
+// e^x for x <= 0 (see the file comment).
+__device__ float texp(float x) {
+  if (!(x >= -80.f)) return 0.f;
+  const float kLog2e = __uint_as_float(0x3FB8AA3Bu), kLn2Hi = __uint_as_float(0x3F317200u),
+              kLn2Lo = __uint_as_float(0x35BFBE8Eu);
+  const float c[8] = {__uint_as_float(0x3F800000u), __uint_as_float(0x3F800000u), __uint_as_float(0x3F000000u),
+                      __uint_as_float(0x3E2AAAABu), __uint_as_float(0x3D2AAAABu), __uint_as_float(0x3C088889u),
+                      __uint_as_float(0x3AB60B61u), __uint_as_float(0x39500D01u)};
+  const float t = __fmul_rn(x, kLog2e);
+  const float n = rintf(t);
+  float r = __fsub_rn(x, __fmul_rn(n, kLn2Hi));
+  r = __fsub_rn(r, __fmul_rn(n, kLn2Lo));
+  float p = c[7];
+#pragma unroll
+  for (int k = 6; k >= 0; --k) p = __fadd_rn(__fmul_rn(p, r), c[k]);
+  int ni = (int)n;
+  ni = ni < -126 ? -126 : (ni > 127 ? 127 : ni);
+  return __fmul_rn(p, __int_as_float((ni + 127) << 23));
+}
+
+// Top-64 of up to 256 * E items held E per thread, items of thread t preceding those of
+// thread t+1 in index order. Keys are ord16 values (0 = padding). Result in LDS out_k/out_i
+// (64 entries, value descending then index ascending); needs blockDim.x == 256.
+template <int E>
+__device__ void select_top64(const uint32_t (&k16)[E], const uint32_t (&idx)[E], uint32_t* out_k, uint32_t* out_i) {
+  __shared__ int hist[256];
+  __shared__ uint32_t sel_k[kCand], sel_i[kCand];
+  __shared__ uint32_t s_bin, s_above;
+  const int tid = threadIdx.x;
+  uint32_t prefix = 0, prefix_mask = 0;
+  int remaining = kCand;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int shift = pass == 0 ? 8 : 0;
+    hist[tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if ((k16[e] & prefix_mask) == prefix) atomicAdd(&hist[(k16[e] >> shift) & 0xFF], 1);
+    __syncthreads();
+    if (tid < 64) {
+      // lane l owns bins 4l..4l+3; find the bin where the count from the top reaches `remaining`
+      const int h0 = hist[4 * tid], h1 = hist[4 * tid + 1], h2 = hist[4 * tid + 2], h3 = hist[4 * tid + 3];
+      const int s = h0 + h1 + h2 + h3;
+      int above = s;  // inclusive suffix sum over lanes >= tid
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_down(above, o);
+        if (tid + o < 64) above += y;
+      }
+      const int strictly_above = above - s;  // items in bins of higher lanes
+      if (strictly_above < remaining && above >= remaining) {
+        int acc = strictly_above, b = 3;
+        const int hh[4] = {h0, h1, h2, h3};
+        while (b > 0 && acc + hh[b] < remaining) acc += hh[b--];
+        s_bin = 4 * tid + b;
+        s_above = acc;
+      }
+      if (tid == 0 && above < remaining) {  // fewer items than 64: take everything
+        s_bin = 0;
+        s_above = above - h0;
+      }
+    }
+    __syncthreads();
+    prefix |= s_bin << shift;
+    prefix_mask |= 0xFFu << shift;
+    remaining -= s_above;
+    __syncthreads();
+  }
+  const uint32_t T = prefix;
+  // ties at T are taken in index order: rank them with a block scan
+  int ties = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) ties += k16[e] == T;
+  int tot;
+  int tie_rank = block_exclusive_scan(ties, &tot);
+  int nsel = 0;
+  bool take[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    take[e] = k16[e] > T || (k16[e] == T && tie_rank < remaining);
+    if (k16[e] == T) ++tie_rank;
+    nsel += take[e];
+  }
+  int pos = block_exclusive_scan(nsel, &tot);
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (take[e] && pos < kCand) {
+      sel_k[pos] = k16[e];
+      sel_i[pos] = idx[e];
+      ++pos;
+    }
+  if (tid >= tot && tid < kCand) {  // fewer than 64 items
+    sel_k[tid] = 0;
+    sel_i[tid] = 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // bitonic sort of 64 (value desc, index asc) keys across the lanes of wave 0
+    uint64_t key = vkey(sel_k[tid], sel_i[tid]);
+    for (int size = 2; size <= 64; size <<= 1)
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const uint64_t other = __shfl_xor(key, stride);
+        const bool desc = (tid & size) == 0;  // final order: descending
+        const bool lower = (tid & stride) == 0;
+        const bool keep_max = desc == lower;
+        key = keep_max ? (other > key ? other : key) : (other < key ? other : key);
+      }
+    out_k[tid] = (uint32_t)(key >> 32);
+    out_i[tid] = vkey_idx(key);
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------ accept outputs
+
+struct AcceptOut {
+  int64_t* pred;        // [M] target token per row (may be null)
+  int64_t* n_accepted;  // [1]
+  int64_t* tok;         // [1] token after the accepted drafts (correction or bonus)
+  int64_t* pos;         // [1] device position, advanced by n + 1
+  int64_t* slot;        // [1] recurrent-state slot to keep (n for chains, best node for trees)
+  int64_t* tokens;      // [M] accepted drafts then tok; -1 beyond
+  int64_t* commit;      // [M] chains: positions pos..pos+n; trees: node indices root..best; -1 beyond
+};
+
+// Engine._verify_step (tokenrush/model.py:302-312): match = pred[:K] == spec[1:M],
+// n = leading matches, tok = pred[n], pos += n + 1, slot = n.
+__device__ void finish_chain(const int64_t* pred, const int64_t* spec, int M, const AcceptOut& o) {
+  int n = 0;
+  while (n < M - 1 && pred[n] == spec[n + 1]) ++n;
+  const int64_t base = *o.pos;
+  const int64_t t = pred[n];
+  *o.n_accepted = n;
+  *o.tok = t;
+  *o.pos = base + n + 1;
+  *o.slot = n;
+  for (int i = 0; i < M; ++i) {
+    o.tokens[i] = i < n ? spec[i + 1] : (i == n ? t : -1);
+    o.commit[i] = i <= n ? base + i : -1;
+  }
+}
+
+// Longest accepted root path of a draft tree (bench/tree_accept.py:91-100): node 0 is the
+// root; node i > 0 (parent[i] < i) is accepted when its token equals the prediction of its
+// parent's row and the parent is accepted. Deepest accepted node wins, lowest index on ties.
+__device__ void finish_tree(const int64_t* pred, const int64_t* node_tok, const int32_t* parent, int M,
+                            const AcceptOut& o) {
+  bool ok[32];
+  int depth[32];
+  ok[0] = true;
+  depth[0] = 0;
+  int best = 0;
+  for (int i = 1; i < M; ++i) {
+    const int p = parent[i];
+    const bool valid = p >= 0 && p < i;  // a malformed parent array accepts nothing below it
+    depth[i] = valid ? depth[p] + 1 : 0;
+    ok[i] = valid && ok[p] && node_tok[i] == pred[p];
+    if (ok[i] && depth[i] > depth[best]) best = i;
+  }
+  const int n = depth[best];
+  int path[32];
+  for (int j = best, d = n; d >= 0; --d) {
+    path[d] = j;
+    j = d > 0 ? parent[j] : 0;
+  }
+  const int64_t base = *o.pos;
+  const int64_t t = pred[best];
+  *o.n_accepted = n;
+  *o.tok = t;
+  *o.pos = base + n + 1;
+  *o.slot = best;
+  for (int i = 0; i < M; ++i) {
+    o.tokens[i] = i < n ? node_tok[path[i + 1]] : (i == n ? t : -1);
+    o.commit[i] = i <= n ? path[i] : -1;
+  }
+}
+
+// ------------------------------------------------------------------ argmax kernel (greedy, tree)
+
+enum { FIN_NONE = 0, FIN_CHAIN = 1, FIN_TREE = 2 };
+
+struct ArgmaxArgs {
+  const uint16_t* logits;  // bf16 [M, V]
+  int M, V, nch, fin;
+  const int64_t* spec;     // chain: committed + drafts [M]; tree: node tokens [M]
+  const int32_t* parent;   // tree: [M]
+  uint64_t* keys;          // ws [M * nch]
+  int64_t* preds;          // ws [M]
+  float* rowmax;           // ws [M] (row maxima, used by the residual kernels)
+  int* cnt_rows;           // ws [M]
+  int* cnt_all;            // ws [1]
+  AcceptOut o;
+};
+
+__global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
+  const int row = blockIdx.x / a.nch, ch = blockIdx.x % a.nch;
+  const int beg = ch * kTopChunk;
+  const uint16_t* lg = a.logits + (size_t)row * a.V;
+  uint64_t best = 0;
+  for (int i = beg + threadIdx.x; i < min(a.V, beg + kTopChunk); i += blockDim.x) {
+    const uint64_t k = vkey(ord16(lg[i]), i);
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  __shared__ uint64_t wmax[4];
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) best = wmax[w] > best ? wmax[w] : best;
+    ws_st(a.keys + blockIdx.x, best);
+  }
+  if (!arrive_last(a.cnt_rows + row, a.nch)) return;
+  if (threadIdx.x < 64) {
+    uint64_t b = 0;
+    for (int c = threadIdx.x; c < a.nch; c += 64) {
+      const uint64_t k = ws_ld(a.keys + (size_t)row * a.nch + c);
+      b = k > b ? k : b;
+    }
+    b = wave_max_u64(b);
+    if (threadIdx.x == 0) {
+      const int64_t idx = vkey_idx(b);
+      if (a.o.pred) a.o.pred[row] = idx;
+      ws_st(a.preds + row, idx);
+      if (a.rowmax) ws_st(a.rowmax + row, bf16_bits_to_f32(unord16((uint32_t)(b >> 32))));
+    }
+  }
+  if (!arrive_last(a.cnt_all, a.M)) return;
+  if (threadIdx.x == 0 && a.fin != FIN_NONE) {
+    int64_t pred[32];
+    for (int i = 0; i < a.M; ++i) pred[i] = ws_ld(a.preds + i);
+    if (a.fin == FIN_CHAIN)
+      finish_chain(pred, a.spec, a.M, a.o);
+    else
+      finish_tree(pred, a.spec, a.parent, a.M, a.o);
+  }
+}
+
+// ------------------------------------------------------------------ sample kernel (sample.py:30-51)
+
+struct SampleArgs {
+  const uint16_t* logits;
+  int M, V, nch, fin;
+  const float* temperature;  // [1] device (0 = greedy)
+  const float* top_p;        // [1]
+  const int64_t* top_k;      // [1]
+  const float* u;            // [M] uniforms in [0, 1)
+  const int64_t* spec;       // chain: committed + drafts [M]
+  uint32_t* cand;            // ws [M * nch * 64 * 2] (key16, index)
+  int64_t* preds;            // ws [M]
+  int* cnt_rows;
+  int* cnt_all;
+  int64_t* out;              // [M] sampled tokens (may be null)
+  AcceptOut o;
+};
+
+// One row's pick from its sorted top-64 (value desc, index asc), by lane 0; sequential fp32
+// arithmetic as the file comment states.
+__device__ int64_t sample_pick(const uint32_t* tk, const uint32_t* ti, float T, float top_p, int64_t top_k, float u) {
+  const int64_t greedy = ti[0];
+  if (!(T > 0.f)) return greedy;
+  const float temp = T > __uint_as_float(0x358637BDu) ? T : __uint_as_float(0x358637BDu);
+  float v[kCand], p[kCand];
+  for (int i = 0; i < kCand; ++i) v[i] = __fdiv_rn(bf16_bits_to_f32(unord16(tk[i])), temp);
+  float Z = 0.f;
+  for (int i = 0; i < kCand; ++i) {
+    p[i] = texp(__fsub_rn(v[i], v[0]));
+    Z = __fadd_rn(Z, p[i]);
+  }
+  float cum = 0.f, cum2 = 0.f;
+  for (int i = 0; i < kCand; ++i) {
+    p[i] = __fdiv_rn(p[i], Z);
+    cum = __fadd_rn(cum, p[i]);
+    const bool keep = __fsub_rn(cum, p[i]) < top_p && i < top_k;
+    if (!keep) p[i] = 0.f;
+    cum2 = __fadd_rn(cum2, p[i]);
+    v[i] = cum2;  // reuse: running sums of the kept mass
+  }
+  const float target = __fmul_rn(u, cum2);
+  int pick = 0;
+  for (int i = 0; i < kCand; ++i) pick += v[i] < target;
+  if (pick > kCand - 1) pick = kCand - 1;
+  return ti[pick];
+}
+
+__global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
+  constexpr int E = kTopChunk / 256;
+  __shared__ uint32_t tk[kCand], ti[kCand];
+  const int row = blockIdx.x / a.nch, ch = blockIdx.x % a.nch;
+  const int beg = ch * kTopChunk;
+  const uint16_t* lg = a.logits + (size_t)row * a.V;
+  uint32_t k16[E], idx[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = beg + threadIdx.x * E + e;
+    idx[e] = i;
+    k16[e] = i < a.V ? ord16(lg[i]) : 0u;
+  }
+  select_top64<E>(k16, idx, tk, ti);
+  uint32_t* mine = a.cand + ((size_t)row * a.nch + ch) * kCand * 2;
+  if (threadIdx.x < kCand) {
+    ws_st(mine + 2 * threadIdx.x, tk[threadIdx.x]);
+    ws_st(mine + 2 * threadIdx.x + 1, ti[threadIdx.x]);
+  }
+  if (!arrive_last(a.cnt_rows + row, a.nch)) return;
+  // merge: the nch sorted lists in chunk order keep equal values in index order
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int c = threadIdx.x * E + e;  // candidate number = chunk * 64 + rank
+    if (c < a.nch * kCand) {
+      const uint32_t* src = a.cand + (size_t)row * a.nch * kCand * 2 + 2 * c;
+      k16[e] = ws_ld(src);
+      idx[e] = ws_ld(src + 1);
+    } else {
+      k16[e] = 0;
+      idx[e] = 0xFFFFFFFFu;
+    }
+  }
+  select_top64<E>(k16, idx, tk, ti);
+  if (threadIdx.x == 0) {
+    const int64_t t = sample_pick(tk, ti, *a.temperature, *a.top_p, *a.top_k, a.u[row]);
+    if (a.out) a.out[row] = t;
+    ws_st(a.preds + row, t);
+  }
+  if (!arrive_last(a.cnt_all, a.M)) return;
+  if (threadIdx.x == 0 && a.fin == FIN_CHAIN) {
+    int64_t pred[32];
+    for (int i = 0; i < a.M; ++i) pred[i] = ws_ld(a.preds + i);
+    if (a.o.pred)
+      for (int i = 0; i < a.M; ++i) a.o.pred[i] = pred[i];
+    finish_chain(pred, a.spec, a.M, a.o);
+  }
+}
+
+// ------------------------------------------------------------------ residual rejection sampling
+
+// Phase 2: per (row, 1024-chunk) run and chunk sums of e = texp(l - rowmax); per row Z; then
+// the accept tests u_i q_i(d_i) < e_i(d_i) / Z_i.
+struct ResidualArgs {
+  const uint16_t* logits;  // [K+1, V]
+  const float* q;          // [K, V]
+  const int64_t* spec;     // committed + K drafts [K+1]
+  const float* u;          // [K+1]
+  int M, V, nch;           // M = K + 1 rows, nch = 1024-chunks per row
+  const float* rowmax;     // ws [M] (from argmax_kernel)
+  float* chunk_sum;        // ws [M * nch] (phase 2), then [nch] (phase 3)
+  float* Z;                // ws [M]
+  float* e_draft;          // ws [M]
+  int* n_ws;               // ws [1]: accepted drafts, read by phase 3
+  int* cnt_rows;
+  int* cnt_all;
+  AcceptOut o;
+};
+
+// This lane's run (16 elements) of r for chunk ch of row `row`: r = e / Z - q clamped at 0
+// (residual), or e / Z (bonus), or e (phase 2, Z unused). Returns the sequential run sum.
+template <int MODE>  // 0: e, 1: residual, 2: p
+__device__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float Zr, float (&vals)[kRun]) {
+  const uint16_t* lg = a.logits + (size_t)row * a.V;
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < kRun; ++e) {
+    const int i = ch * kChunk + lane * kRun + e;
+    float v = 0.f;
+    if (i < a.V) {
+      v = texp(__fsub_rn(bf16_bits_to_f32(lg[i]), mx));
+      if (MODE >= 1) v = __fdiv_rn(v, Zr);
+      if (MODE == 1) {
+        v = __fsub_rn(v, a.q[(size_t)row * a.V + i]);
+        v = v > 0.f ? v : 0.f;
+      }
+    }
+    vals[e] = v;
+    s = __fadd_rn(s, v);
+  }
+  return s;
+}
+
+__device__ float chunk_total(float run_sum, float* lds64) {
+  const int lane = threadIdx.x & 63;
+  lds64[lane] = run_sum;
+  __syncthreads();
+  float t = 0.f;
+  if (lane == 0)
+    for (int i = 0; i < 64; ++i) t = __fadd_rn(t, lds64[i]);
+  __syncthreads();
+  return t;
+}
+
+__global__ __launch_bounds__(64) void residual_phase2_kernel(ResidualArgs a) {
+  __shared__ float lds64[64];
+  const int row = blockIdx.x / a.nch, ch = blockIdx.x % a.nch;
+  const int lane = threadIdx.x;
+  const float mx = ws_ld(a.rowmax + row);
+  float vals[kRun];
+  const float rs = run_values<0>(a, row, ch, lane, mx, 1.f, vals);
+  const float ct = chunk_total(rs, lds64);
+  const int K = a.M - 1;
+  if (row < K) {
+    const int64_t d = a.spec[row + 1];
+    const int base = ch * kChunk + lane * kRun;
+    if (d >= base && d < base + kRun) ws_st(a.e_draft + row, vals[d - base]);
+  }
+  if (lane == 0) ws_st(a.chunk_sum + blockIdx.x, ct);
+  if (!arrive_last(a.cnt_rows + row, a.nch)) return;
+  if (lane == 0) {
+    float z = 0.f;
+    for (int c = 0; c < a.nch; ++c) z = __fadd_rn(z, ws_ld(a.chunk_sum + (size_t)row * a.nch + c));
+    ws_st(a.Z + row, z);
+  }
+  if (!arrive_last(a.cnt_all, a.M)) return;
+  if (lane == 0) {
+    int n = 0;
+    while (n < K) {
+      const int64_t d = a.spec[n + 1];
+      if (d < 0 || d >= a.V) break;  // an out-of-vocabulary draft is rejected
+      const float pd = __fdiv_rn(ws_ld(a.e_draft + n), ws_ld(a.Z + n));
+      if (__fmul_rn(a.u[n], a.q[(size_t)n * a.V + d]) < pd)
+        ++n;
+      else
+        break;
+    }
+    ws_st(a.n_ws, n);
+  }
+}
+
+// Phase 3: one row j = n (the first rejected draft's row, or the bonus row K): chunk sums of
+// r, then the last workgroup draws the token with u[K] by a blocked inverse-CDF search.
+__global__ __launch_bounds__(64) void residual_phase3_kernel(ResidualArgs a) {
+  __shared__ float lds64[64];
+  __shared__ float runs[64];
+  const int ch = blockIdx.x, lane = threadIdx.x;
+  const int K = a.M - 1;
+  const int j = ws_ld(a.n_ws);
+  const float mx = ws_ld(a.rowmax + j), Zj = ws_ld(a.Z + j);
+  float vals[kRun];
+  const float rs = j < K ? run_values<1>(a, j, ch, lane, mx, Zj, vals) : run_values<2>(a, j, ch, lane, mx, Zj, vals);
+  const float ct = chunk_total(rs, lds64);
+  if (lane == 0) ws_st(a.chunk_sum + ch, ct);
+  if (!arrive_last(a.cnt_all, a.nch)) return;
+  __shared__ int s_pick_chunk;
+  __shared__ float s_acc;
+  __shared__ float s_target;
+  __shared__ int s_degenerate;
+  if (lane == 0) {
+    float R = 0.f;
+    for (int c = 0; c < a.nch; ++c) R = __fadd_rn(R, ws_ld(a.chunk_sum + c));
+    s_degenerate = !(R > 0.f);
+    const float target = __fmul_rn(a.u[K], R);
+    // first chunk whose running total exceeds the target; else the last nonzero chunk
+    float cp = 0.f, cp_last = 0.f;
+    int c_found = -1, c_last = -1;
+    for (int c = 0; c < a.nch; ++c) {
+      const float t = ws_ld(a.chunk_sum + c);
+      if (t > 0.f) {
+        c_last = c;
+        cp_last = cp;
+      }
+      if (__fadd_rn(cp, t) > target) {
+        c_found = c;
+        break;
+      }
+      cp = __fadd_rn(cp, t);
+    }
+    s_pick_chunk = c_found >= 0 ? c_found : c_last;
+    s_acc = c_found >= 0 ? cp : cp_last;
+    s_target = target;
+  }
+  __syncthreads();
+  int pick = -1;
+  if (!s_degenerate) {
+    const int c = s_pick_chunk;
+    const float rsum = j < K ? run_values<1>(a, j, c, lane, mx, Zj, vals) : run_values<2>(a, j, c, lane, mx, Zj, vals);
+    runs[lane] = rsum;
+    lds64[lane] = 0.f;
+    __syncthreads();
+    // lane 0 finds the run, then the element, sequentially
+    __shared__ int s_run;
+    __shared__ float s_run_acc;
+    if (lane == 0) {
+      float acc = s_acc, acc_last = s_acc;
+      int t_found = -1, t_last = -1;
+      for (int t = 0; t < 64; ++t) {
+        if (runs[t] > 0.f) {
+          t_last = t;
+          acc_last = acc;
+        }
+        if (__fadd_rn(acc, runs[t]) > s_target) {
+          t_found = t;
+          break;
+        }
+        acc = __fadd_rn(acc, runs[t]);
+      }
+      s_run = t_found >= 0 ? t_found : t_last;
+      s_run_acc = t_found >= 0 ? acc : acc_last;
+    }
+    __syncthreads();
+    if (lane == s_run) {
+      float acc = s_run_acc;
+      int last_nz = -1;
+      for (int e = 0; e < kRun; ++e) {
+        if (vals[e] > 0.f) last_nz = e;
+        acc = __fadd_rn(acc, vals[e]);
+        if (acc > s_target) {
+          pick = c * kChunk + lane * kRun + e;
+          break;
+        }
+      }
+      if (pick < 0) pick = c * kChunk + lane * kRun + last_nz;
+      lds64[0] = __int_as_float(pick);
+    }
+    __syncthreads();
+    pick = __float_as_int(lds64[0]);
+  } else {
+    // degenerate residual (all zero): fall back to the row's argmax
+    pick = -2;
+  }
+  if (lane == 0) {
+    if (pick == -2) {
+      const uint16_t* lg = a.logits + (size_t)j * a.V;
+      uint64_t b = 0;
+      for (int i = 0; i < a.V; ++i) {
+        const uint64_t k = vkey(ord16(lg[i]), i);
+        b = k > b ? k : b;
+      }
+      pick = (int)vkey_idx(b);
+    }
+    const int n = j;
+    const int64_t base = *a.o.pos;
+    *a.o.n_accepted = n;
+    *a.o.tok = pick;
+    *a.o.pos = base + n + 1;
+    *a.o.slot = n;
+    for (int i = 0; i < a.M; ++i) {
+      a.o.tokens[i] = i < n ? a.spec[i + 1] : (i == n ? pick : -1);
+      a.o.commit[i] = i <= n ? base + i : -1;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ tree KV commit
+
+// Moves the accepted path's rows to consecutive positions: for every plane (layer x kv head),
+// row base + commit[t] -> row base + t for t = 1..n, where base = pos - n - 1 (pos already
+// advanced by the accept kernel). Rows are read into registers before any is written.
+__global__ void commit_rows_kernel(uint8_t* data, int planes, long plane_stride, int row_bytes, const int64_t* pos,
+                                   const int64_t* n_accepted, const int64_t* commit, int max_n) {
+  const int plane = blockIdx.x;
+  if (plane >= planes) return;
+  const int n = (int)*n_accepted;
+  const int64_t base = *pos - n - 1;
+  const int64_t max_len = plane_stride / row_bytes;
+  for (int t = 1; t <= n && t <= max_n; ++t)  // rows outside the cache: commit nothing
+    if (base < 0 || base + commit[t] >= max_len || base + t >= max_len || commit[t] < 0) return;
+  uint8_t* p = data + (size_t)plane * plane_stride;
+  // each thread moves 4-byte words; row_bytes % 4 == 0
+  const int words = row_bytes / 4;
+  for (int w0 = 0; w0 < words; w0 += blockDim.x) {
+    const int w = w0 + threadIdx.x;
+    uint32_t v[32];
+    for (int t = 1; t <= n && t <= max_n; ++t)
+      if (w < words) v[t - 1] = ((const uint32_t*)(p + (size_t)(base + commit[t]) * row_bytes))[w];
+    __syncthreads();
+    for (int t = 1; t <= n && t <= max_n; ++t)
+      if (w < words) ((uint32_t*)(p + (size_t)(base + t) * row_bytes))[w] = v[t - 1];
+    __syncthreads();
+  }
+}
+
+}  // namespace tr
+
+// ------------------------------------------------------------------ C ABI
+using namespace tr;
+
+namespace {
+
+// Workspace layout (bytes): [0, 4096) int32 counters (zero between calls);
+// then the largest of the per-kernel scratch areas.
+constexpr size_t kCntBytes = 4096;
+
+int nch_top(int V) { return (V + kTopChunk - 1) / kTopChunk; }
+int nch_run(int V) { return (V + kChunk - 1) / kChunk; }
+
+size_t scratch_bytes(int M, int V) {
+  const size_t argmax = (size_t)M * nch_top(V) * 8 + (size_t)M * 8 + (size_t)M * 4;
+  const size_t samp = (size_t)M * nch_top(V) * kCand * 8 + (size_t)M * 8;
+  const size_t resid = (size_t)M * nch_run(V) * 4 + (size_t)M * 4 * 3 + 16;
+  size_t m = argmax > samp ? argmax : samp;
+  m = m > resid + argmax ? m : resid + argmax;
+  return (m + 255) & ~(size_t)255;
+}
+
+struct WsView {
+  int* cnt;
+  char* scratch;
+};
+
+bool ws_view(void* ws, size_t bytes, int M, int V, WsView* v) {
+  if (!ws || bytes < kCntBytes + scratch_bytes(M, V)) return false;
+  v->cnt = (int*)ws;
+  v->scratch = (char*)ws + kCntBytes;
+  return true;
+}
+
+bool check_mv(int M, int V) { return M >= 1 && M <= 32 && V >= kCand && nch_top(V) <= 64; }
+
+AcceptOut make_out(int64_t* pred, int64_t* n, int64_t* tok, int64_t* pos, int64_t* slot, int64_t* tokens,
+                   int64_t* commit) {
+  AcceptOut o;
+  o.pred = pred;
+  o.n_accepted = n;
+  o.tok = tok;
+  o.pos = pos;
+  o.slot = slot;
+  o.tokens = tokens;
+  o.commit = commit;
+  return o;
+}
+
+// counters: [0, 32) rows of the first kernel, [32] all-rows of the first kernel,
+// [64, 96) rows of the residual phase 2, [96] its all-rows, [128] phase 3.
+int launch_argmax(const void* logits, int M, int V, int fin, const int64_t* spec, const int32_t* parent,
+                  const WsView& w, float* rowmax, const AcceptOut& o, hipStream_t st) {
+  ArgmaxArgs a;
+  a.logits = (const uint16_t*)logits;
+  a.M = M;
+  a.V = V;
+  a.nch = nch_top(V);
+  a.fin = fin;
+  a.spec = spec;
+  a.parent = parent;
+  a.keys = (uint64_t*)w.scratch;
+  a.preds = (int64_t*)(w.scratch + (size_t)M * a.nch * 8);
+  a.rowmax = rowmax;
+  a.cnt_rows = w.cnt;
+  a.cnt_all = w.cnt + 32;
+  a.o = o;
+  hipLaunchKernelGGL(argmax_kernel, dim3(M * a.nch), dim3(256), 0, st, a);
+  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t tr_accept_workspace_bytes(int M, int V) {
+  if (!check_mv(M, V)) return 0;
+  return kCntBytes + scratch_bytes(M, V);
+}
+
+int tr_argmax_rows(const void* logits, int M, int V, void* ws, size_t ws_bytes, int64_t* pred, void* stream) {
+  WsView w;
+  if (!check_mv(M, V)) return TR_ERR_SHAPE;
+  if (!logits || !pred || !ws_view(ws, ws_bytes, M, V, &w)) return TR_ERR_ARG;
+  return launch_argmax(logits, M, V, FIN_NONE, nullptr, nullptr, w, nullptr,
+                       make_out(pred, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr), (hipStream_t)stream);
+}
+
+int tr_accept_greedy(const void* logits, int M, int V, const int64_t* spec_toks, void* ws, size_t ws_bytes,
+                     int64_t* pred, int64_t* n_accepted, int64_t* tok, int64_t* pos, int64_t* slot, int64_t* tokens,
+                     int64_t* commit, void* stream) {
+  WsView w;
+  if (!check_mv(M, V)) return TR_ERR_SHAPE;
+  if (!logits || !spec_toks || !n_accepted || !tok || !pos || !slot || !tokens || !commit ||
+      !ws_view(ws, ws_bytes, M, V, &w))
+    return TR_ERR_ARG;
+  return launch_argmax(logits, M, V, FIN_CHAIN, spec_toks, nullptr, w, nullptr,
+                       make_out(pred, n_accepted, tok, pos, slot, tokens, commit), (hipStream_t)stream);
+}
+
+int tr_accept_tree(const void* logits, int M, int V, const int64_t* node_toks, const int32_t* parent, void* ws,
+                   size_t ws_bytes, int64_t* pred, int64_t* n_accepted, int64_t* tok, int64_t* pos, int64_t* slot,
+                   int64_t* tokens, int64_t* commit, void* stream) {
+  WsView w;
+  if (!check_mv(M, V)) return TR_ERR_SHAPE;
+  if (!logits || !node_toks || !parent || !n_accepted || !tok || !pos || !slot || !tokens || !commit ||
+      !ws_view(ws, ws_bytes, M, V, &w))
+    return TR_ERR_ARG;
+  return launch_argmax(logits, M, V, FIN_TREE, node_toks, parent, w, nullptr,
+                       make_out(pred, n_accepted, tok, pos, slot, tokens, commit), (hipStream_t)stream);
+}
+
+static int launch_sample(const void* logits, int M, int V, int fin, const float* temperature, const float* top_p,
+                         const int64_t* top_k, const float* u, const int64_t* spec, void* ws, size_t ws_bytes,
+                         int64_t* out, const AcceptOut& o, hipStream_t st) {
+  WsView w;
+  if (!check_mv(M, V)) return TR_ERR_SHAPE;
+  if (!logits || !temperature || !top_p || !top_k || !u || !ws_view(ws, ws_bytes, M, V, &w)) return TR_ERR_ARG;
+  SampleArgs a;
+  a.logits = (const uint16_t*)logits;
+  a.M = M;
+  a.V = V;
+  a.nch = nch_top(V);
+  a.fin = fin;
+  a.temperature = temperature;
+  a.top_p = top_p;
+  a.top_k = top_k;
+  a.u = u;
+  a.spec = spec;
+  a.cand = (uint32_t*)w.scratch;
+  a.preds = (int64_t*)(w.scratch + (size_t)M * a.nch * kCand * 8);
+  a.cnt_rows = w.cnt;
+  a.cnt_all = w.cnt + 32;
+  a.out = out;
+  a.o = o;
+  hipLaunchKernelGGL(sample_kernel, dim3(M * a.nch), dim3(256), 0, st, a);
+  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+int tr_sample(const void* logits, int M, int V, const float* temperature, const float* top_p, const int64_t* top_k,
+              const float* u, void* ws, size_t ws_bytes, int64_t* out, void* stream) {
+  if (!out) return TR_ERR_ARG;
+  return launch_sample(logits, M, V, FIN_NONE, temperature, top_p, top_k, u, nullptr, ws, ws_bytes, out,
+                       make_out(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr), (hipStream_t)stream);
+}
+
+int tr_accept_sample(const void* logits, int M, int V, const int64_t* spec_toks, const float* temperature,
+                     const float* top_p, const int64_t* top_k, const float* u, void* ws, size_t ws_bytes,
+                     int64_t* pred, int64_t* n_accepted, int64_t* tok, int64_t* pos, int64_t* slot, int64_t* tokens,
+                     int64_t* commit, void* stream) {
+  if (!spec_toks || !n_accepted || !tok || !pos || !slot || !tokens || !commit) return TR_ERR_ARG;
+  return launch_sample(logits, M, V, FIN_CHAIN, temperature, top_p, top_k, u, spec_toks, ws, ws_bytes, nullptr,
+                       make_out(pred, n_accepted, tok, pos, slot, tokens, commit), (hipStream_t)stream);
+}
+
+int tr_accept_residual(const void* logits, int M, int V, const float* q, const int64_t* spec_toks, const float* u,
+                       void* ws, size_t ws_bytes, int64_t* n_accepted, int64_t* tok, int64_t* pos, int64_t* slot,
+                       int64_t* tokens, int64_t* commit, void* stream) {
+  WsView w;
+  if (!check_mv(M, V) || M < 2) return TR_ERR_SHAPE;
+  if (!logits || !q || !spec_toks || !u || !n_accepted || !tok || !pos || !slot || !tokens || !commit ||
+      !ws_view(ws, ws_bytes, M, V, &w))
+    return TR_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  // phase 1: row maxima (argmax kernel, no finish)
+  const size_t am = (size_t)M * nch_top(V) * 8 + (size_t)M * 8;
+  float* rowmax = (float*)(w.scratch + am);
+  int rc = launch_argmax(logits, M, V, FIN_NONE, nullptr, nullptr, w, rowmax,
+                         make_out(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr), st);
+  if (rc) return rc;
+  ResidualArgs a;
+  a.logits = (const uint16_t*)logits;
+  a.q = q;
+  a.spec = spec_toks;
+  a.u = u;
+  a.M = M;
+  a.V = V;
+  a.nch = nch_run(V);
+  a.rowmax = rowmax;
+  char* r = w.scratch + am + (size_t)M * 4;
+  a.chunk_sum = (float*)r;
+  r += (size_t)M * a.nch * 4;
+  a.Z = (float*)r;
+  a.e_draft = a.Z + M;
+  a.n_ws = (int*)(a.e_draft + M);
+  a.cnt_rows = w.cnt + 64;
+  a.cnt_all = w.cnt + 96;
+  a.o = make_out(nullptr, n_accepted, tok, pos, slot, tokens, commit);
+  hipLaunchKernelGGL(residual_phase2_kernel, dim3(M * a.nch), dim3(64), 0, st, a);
+  if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
+  a.cnt_all = w.cnt + 128;
+  hipLaunchKernelGGL(residual_phase3_kernel, dim3(a.nch), dim3(64), 0, st, a);
+  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+int tr_commit_rows(void* data, int planes, long plane_stride_bytes, int row_bytes, const int64_t* pos,
+                   const int64_t* n_accepted, const int64_t* commit, int max_n, void* stream) {
+  if (!data || !pos || !n_accepted || !commit) return TR_ERR_ARG;
+  if (planes < 1 || row_bytes < 4 || row_bytes % 4 || max_n < 0 || max_n > 32) return TR_ERR_SHAPE;
+  hipLaunchKernelGGL(commit_rows_kernel, dim3(planes), dim3(256), 0, (hipStream_t)stream, (uint8_t*)data, planes,
+                     plane_stride_bytes, row_bytes, pos, n_accepted, commit, max_n);
+  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+}  // extern "C"

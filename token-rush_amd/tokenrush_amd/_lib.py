@@ -31,6 +31,14 @@ SIGNATURES = {
     "tr_pack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "tr_unpack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "tr_dequant_int4": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "tr_accept_workspace_bytes": (_S, [_I, _I]),
+    "tr_argmax_rows": (_I, [_P, _I, _I, _P, _S, _P, _P]),
+    "tr_accept_greedy": (_I, [_P, _I, _I, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tr_accept_tree": (_I, [_P, _I, _I, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tr_sample": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _S, _P, _P]),
+    "tr_accept_sample": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tr_accept_residual": (_I, [_P, _I, _I, _P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P]),
+    "tr_commit_rows": (_I, [_P, _I, ctypes.c_long, _I, _P, _P, _P, _I, _P]),
 }
 
 _lib = None
