@@ -3,19 +3,24 @@
 
 Workload: one layer's int4 g128 projection set -- QKV-like 7168x5120,
 O 5120x6144, fused gate/up 34816x5120, down 5120x17408, fp16 scale/min -- scored against
-M = 8 verify rows (1 committed + 7 drafts), bf16 x ~ N(0, 1), synthetic seeded data.
-A "step" is one pass over the layer set: 4 GEMM launches, each captured in a hipGraph.
-Steps cycle through enough distinct weight copies (>= 1 GiB) that every step reads its
-weights from HBM, not from the 256 MB MALL.
+M = 8 verify rows (1 committed + 7 drafts), bf16 x ~ N(0, 1), synthetic seeded data. As in the
+reference engine (weights.py:163-174, model.py:211-260), the hidden-sized outputs (O, down) are
+produced as fp32 split-K partials (QLinear.partials) and the others as bf16 (QLinear.__call__).
+A "step" is one pass over the layer set: 4 kernel launches captured in one hipGraph. Steps
+cycle through enough distinct weight copies (>= 1 GiB) that every step reads its weights from
+HBM, not from the 256 MB MALL.
 
-value = whole-job algorithmic bytes / wall time of the timed steps (GB/s), bytes per GEMM
-  N*K/2 + 4*N*K/128 + 2*M*K + 2*M*N.
-roofline: the dominant kernel (gate/up) -- its algorithmic bytes / its average duration
-  measured with HIP events on the launch stream inside the timed region, vs 8 TB/s.
-cpu_baseline: the CPU oracle (numpy dequantize + matmul, the reference's torch path
-  restated) on one layer set at M = 8, single thread, on this host.
+value       whole-job algorithmic bytes / wall time of the timed steps (GB/s); bytes per GEMM
+            N*K/2 + 4*N*K/128 + 2*M*K + (2*M*N bf16 out | 4*S*M*N fp32 partials).
+roofline    the dominant kernel (gate/up, 53% of the bytes): its algorithmic bytes / its mean
+            duration, measured with HIP events around a graph of back-to-back launches of that
+            kernel alone over all weight copies, on the launch stream; vs 8 TB/s.
+accept      on-device accept latency (BASELINE config 3 and 4): mean per launch over a graph of
+            back-to-back calls.
+cpu_baseline  the CPU oracle (numpy dequantize + matmul: the reference's torch path restated)
+            on one layer set at M = 8, one thread, on this host.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
 import argparse
 import json
@@ -27,64 +32,116 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "token-rush_amd"))
 
 HBM_PEAK_GBS = 8000.0
-LAYER_SET = [("qkv", 7168, 5120), ("o", 5120, 6144), ("gate_up", 34816, 5120), ("down", 5120, 17408)]
+# (name, N, K, partial): partial = the reference computes this projection as split-K partials
+LAYER_SET = [("qkv", 7168, 5120, False), ("o", 5120, 6144, True), ("gate_up", 34816, 5120, False),
+             ("down", 5120, 17408, True)]
 M_VERIFY = 8
+V = 248320
 
 
-def algo_bytes(N, K, M, out_bytes=2):
-    return N * K // 2 + 4 * N * K // 128 + 2 * M * K + out_bytes * M * N
+def algo_bytes(N, K, M, slots=None):
+    out = 4 * slots * M * N if slots else 2 * M * N
+    return N * K // 2 + 4 * N * K // 128 + 2 * M * K + out
 
 
-def make_layer_set(torch, gen, dev):
+def make_layer_set(torch, gfx950, gen, dev):
     ws = []
-    for name, N, K in LAYER_SET:
+    for name, N, K, partial in LAYER_SET:
         q = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=gen)
         s = (torch.rand(N, K // 128, device=dev, generator=gen) * 0.018 + 0.002).half()
         m = (torch.rand(N, K // 128, device=dev, generator=gen) * 0.14 - 0.15).half()
-        ws.append((name, N, K, q, s, m))
+        B, sv, _ = gfx950.pack(q, s, m)
+        gfx950.workspaces(N, dev, K)
+        ws.append((name, N, K, partial, B, sv))
+        del q, s, m
     return ws
 
 
-def time_config(torch, gfx950, copies, M, steps, warmup, dev, gen):
-    """Returns (wall seconds for `steps` steps, {name: mean kernel ms}, bytes per step)."""
-    xs = {K: torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16) for _, _, K in LAYER_SET}
-    graphs = []         # graphs[c][i]: copy c, projection i
-    for ws in copies:
-        row = []
-        for name, N, K, B, s, m in ws:
-            y = gfx950.mul(xs[K], B, s, m)               # warm + allocate outside capture
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                y2 = gfx950.mul(xs[K], B, s, m)
-            row.append((name, g, y2))
-        graphs.append(row)
+def call(gfx950, x, w):
+    name, N, K, partial, B, sv = w
+    return gfx950.mul_partial(x, B, sv) if partial else gfx950.mul(x, B, sv)
+
+
+def graph_of(torch, fn):
+    fn()                                           # warm up + allocate outside capture
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def timed_graph(torch, g, reps=3):
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e-3      # seconds per replay
+
+
+def run_steps(torch, gfx950, copies, M, steps, warmup, gen, dev):
+    """Wall seconds of `steps` layer-set steps (one graph per copy, replayed round robin)."""
+    xs = {K: torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16) for _, _, K, _ in LAYER_SET}
+    graphs = [graph_of(torch, lambda c=c: [call(gfx950, xs[w[2]], w) for w in c]) for c in copies]
     C = len(graphs)
     for i in range(warmup):
-        for _, g, _ in graphs[i % C]:
-            g.replay()
+        graphs[i % C].replay()
     torch.cuda.synchronize()
-    nproj = len(LAYER_SET)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(nproj + 1)] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
-        row = graphs[i % C]
-        ev[i][0].record()
-        for j, (_, g, _) in enumerate(row):
-            g.replay()
-            ev[i][j + 1].record()
+        graphs[i % C].replay()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = {}
-    for j, (name, _, _) in enumerate(graphs[0]):
-        per[name] = sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(steps)) / steps
-    step_bytes = sum(algo_bytes(N, K, M) for _, N, K in LAYER_SET)
-    return wall, per, step_bytes
+    return time.perf_counter() - t0, xs
+
+
+def kernel_means(torch, gfx950, copies, xs, reps=4):
+    """Mean seconds per launch of each projection: a graph of reps x copies back-to-back launches."""
+    out = {}
+    for j, (name, N, K, partial) in enumerate(LAYER_SET):
+        g = graph_of(torch, lambda j=j, K=K: [call(gfx950, xs[K], c[j]) for _ in range(reps) for c in copies])
+        out[name] = timed_graph(torch, g) / (reps * len(copies))
+        del g
+    return out
+
+
+def accept_latency(torch, dev):
+    """Mean microseconds per launch of the accept kernels at BASELINE configs 3 and 4."""
+    from tokenrush_amd.accept import AcceptState, accept_greedy, accept_residual, accept_sampled, accept_tree
+    from tokenrush_amd.sample import SamplingParams, workspace
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    res = {}
+    lg8 = (torch.randn(8, V, device=dev, generator=gen) * 2).to(torch.bfloat16)
+    lg32 = (torch.randn(32, V, device=dev, generator=gen) * 2).to(torch.bfloat16)
+    spec = torch.randint(0, V, (32,), device=dev, generator=gen)
+    q = torch.softmax(torch.randn(7, V, device=dev, generator=gen) * 2, -1).contiguous()
+    u = torch.rand(32, device=dev, generator=gen)
+    parent = torch.tensor([-1] + [max(0, (i - 1) // 4) for i in range(1, 32)], dtype=torch.int32, device=dev)
+    p = SamplingParams(dev)
+    p.set(temperature=1.0, top_p=0.95, top_k=64)
+    st8, st32 = AcceptState(8, dev), AcceptState(32, dev)
+    workspace(32, V, dev)
+    cases = {
+        "greedy_m8": lambda: accept_greedy(lg8, spec, st8),
+        "sampled_m8": lambda: accept_sampled(lg8, spec, p, st8, u[:8]),
+        "residual_m8": lambda: accept_residual(lg8, q, spec, u[:8], st8),
+        "tree_m32": lambda: accept_tree(lg32, spec, parent, st32),
+    }
+    reps = 20
+    for name, fn in cases.items():
+        g = graph_of(torch, lambda fn=fn: [fn() for _ in range(reps)])
+        res[name] = round(timed_graph(torch, g) / reps * 1e6, 2)
+        del g
+    return res
 
 
 def cpu_baseline(M=M_VERIFY):
     """Oracle (numpy, single thread) dequantize + matmul over one layer set at M rows."""
-    import numpy as np
+    import numpy as np  # noqa: F401
     try:
         from threadpoolctl import threadpool_limits
     except ImportError:     # pragma: no cover
@@ -94,7 +151,7 @@ def cpu_baseline(M=M_VERIFY):
     total_bytes, total_s = 0, 0.0
     ctx = threadpool_limits(1) if threadpool_limits else None
     try:
-        for i, (name, N, K) in enumerate(LAYER_SET):
+        for i, (name, N, K, partial) in enumerate(LAYER_SET):
             p, s, m = o.make_weights(N, K, seed=300 + i, dtype="fp16")
             x = o.make_x(M, K, seed=400 + i)
             t0 = time.perf_counter()
@@ -106,45 +163,71 @@ def cpu_baseline(M=M_VERIFY):
         if ctx is not None:
             ctx.__exit__(None, None, None)
     return {"value": round(total_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"one config-2 layer set (4 projections) at M={M}, numpy dequantize (two fp16 roundings) "
-                      f"+ fp64 matmul, {total_s:.1f} s"}
+            "sample": f"one config-2 layer set (4 projections, 178 MB of int4 weights) at M={M}: numpy "
+                      f"dequantize (two fp16 roundings) + fp64 matmul, {total_s:.1f} s"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET],
+                    help="profiling aid: run just this projection's launches (M=8) and exit")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="profiling aid: run a plain 1 GiB device copy (read 1 GiB, write 1 GiB) and exit")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the verify path shards "
-              "column/row-parallel by design, but only the one-GPU kernel is built and measured)", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (how the verify path would "
+              "shard is a design note; only the one-GPU kernels are built and measured)", file=sys.stderr)
         sys.exit(2)
 
     import torch
     from tokenrush_amd import gfx950
     gfx950.ext()                                   # fail loudly if the library is missing
     dev = torch.device("cuda:0")
+    if a.copy_calibration:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
-    copy_bytes = sum(N * K // 2 + 4 * N * K // 128 for _, N, K in LAYER_SET)
+    copy_bytes = sum(N * K // 2 + 4 * N * K // 128 for _, N, K, _ in LAYER_SET)
     n_copies = max(2, -(-(1 << 30) // copy_bytes))  # >= 1 GiB of distinct weights
-    copies = []
-    for _ in range(n_copies):
-        ws = make_layer_set(torch, gen, dev)
-        copies.append([(name, N, K) + gfx950.pack(q, s, m) for name, N, K, q, s, m in ws])
-        del ws
+    copies = [make_layer_set(torch, gfx950, gen, dev) for _ in range(n_copies)]
     torch.cuda.synchronize()
 
-    wall8, per8, bytes8 = time_config(torch, gfx950, copies, M_VERIFY, a.steps, a.warmup, dev, gen)
-    wall1, per1, bytes1 = time_config(torch, gfx950, copies, 1, a.steps, a.warmup, dev, gen)
-    value = bytes8 * a.steps / wall8 / 1e9
-    ms_step = wall8 * 1e3 / a.steps
-    gu = dict((n, (N, K)) for n, N, K in LAYER_SET)["gate_up"]
-    achieved = algo_bytes(gu[0], gu[1], M_VERIFY) / (per8["gate_up"] * 1e-3) / 1e9
-    kern8 = sum(per8.values())
-    kern1 = sum(per1.values())
+    if a.only:
+        j = [n for n, _, _, _ in LAYER_SET].index(a.only)
+        x = torch.randn(M_VERIFY, LAYER_SET[j][2], device=dev, generator=gen).to(torch.bfloat16)
+        for _ in range(max(1, a.steps // n_copies)):
+            for c in copies:
+                call(gfx950, x, c[j])
+        torch.cuda.synchronize()
+        print(json.dumps({"only": a.only, "launches": max(1, a.steps // n_copies) * n_copies}))
+        return
+
+    slots = {name: (gfx950.partial_slots(N, K, M_VERIFY) if partial else None) for name, N, K, partial in LAYER_SET}
+    step_bytes = {M: sum(algo_bytes(N, K, M, slots[n]) for n, N, K, _ in LAYER_SET) for M in (1, 8)}
+
+    wall8, xs8 = run_steps(torch, gfx950, copies, M_VERIFY, a.steps, a.warmup, gen, dev)
+    k8 = kernel_means(torch, gfx950, copies, xs8)
+    wall1, xs1 = run_steps(torch, gfx950, copies, 1, a.steps, a.warmup, gen, dev)
+    k1 = kernel_means(torch, gfx950, copies, xs1)
+    sweep = {}
+    for M in (2, 4, 16, 32):
+        xsM = {K: torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16) for _, _, K, _ in LAYER_SET}
+        sweep[M] = round(sum(kernel_means(torch, gfx950, copies, xsM, reps=2).values()) * 1e6, 2)
+    acc = accept_latency(torch, dev)
+
+    value = step_bytes[8] * a.steps / wall8 / 1e9
+    gu = dict((n, (N, K)) for n, N, K, _ in LAYER_SET)["gate_up"]
+    achieved = algo_bytes(gu[0], gu[1], M_VERIFY) / k8["gate_up"] / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gate_up_m8_traffic.json")
     if os.path.exists(tpath):
@@ -152,21 +235,23 @@ def main():
     out = {
         "metric": "int4 verify GEMM HBM GB/s (% of peak) at M=1,8; verify+accept step latency us",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int4 weights x bf16 -> fp32 acc (fp16 scale/min), bf16 out", "data": "synthetic",
-        "config": {"workload": "BASELINE config 2: one layer set (qkv 7168x5120, o 5120x6144, gate_up 34816x5120, "
-                               "down 5120x17408) at M=8, weights cycled over %d copies" % n_copies,
-                   "M": M_VERIFY, "parallelism": "none (1 GPU)"},
+        "ms_per_step": round(wall8 * 1e3 / a.steps, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int4 x bf16 -> fp32 acc (fp16 scale/min)", "data": "synthetic",
+        "config": {"workload": "BASELINE config 2: one layer set (qkv 7168x5120, o 5120x6144 partials, gate_up "
+                               "34816x5120, down 5120x17408 partials), M=8, weights cycled over %d copies (%.2f GB)"
+                               % (n_copies, n_copies * copy_bytes / 1e9), "M": M_VERIFY, "parallelism": "none"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "kernel_us_m8": {k: round(v * 1e3, 2) for k, v in per8.items()},
-        "kernel_us_m1": {k: round(v * 1e3, 2) for k, v in per1.items()},
-        "kernel_gbs_m8": {n: round(algo_bytes(N, K, 8) / (per8[n] * 1e-3) / 1e9, 1) for n, N, K in LAYER_SET},
-        "kernel_gbs_m1": {n: round(algo_bytes(N, K, 1) / (per1[n] * 1e-3) / 1e9, 1) for n, N, K in LAYER_SET},
-        "value_m1": round(bytes1 * a.steps / wall1 / 1e9, 2),
-        "m8_over_m1_kernel_time": round(kern8 / kern1, 4),
+        "value_m1": round(step_bytes[1] * a.steps / wall1 / 1e9, 2),
+        "kernel_us_m8": {k: round(v * 1e6, 2) for k, v in k8.items()},
+        "kernel_us_m1": {k: round(v * 1e6, 2) for k, v in k1.items()},
+        "kernel_gbs_m8": {n: round(algo_bytes(N, K, 8, slots[n]) / k8[n] / 1e9, 1) for n, N, K, _ in LAYER_SET},
+        "m8_over_m1": round(sum(k8.values()) / sum(k1.values()), 4),
+        "layer_set_us_by_M": {1: round(sum(k1.values()) * 1e6, 2), 8: round(sum(k8.values()) * 1e6, 2), **sweep},
+        "accept_us": acc,
+        "verify_accept_us_m8": round(sum(k8.values()) * 1e6 + acc["greedy_m8"], 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "int4_gemm_kernel gate_up 34816x5120 M=8"},
+                     "kernel": "int4_gemm_kernel gate_up 34816x5120 M=8 (%.2f us)" % (k8["gate_up"] * 1e6)},
     }
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline()

@@ -32,7 +32,7 @@ extern "C" {
  * `out` (bf16 [M, N]) and `partials` (fp32 [n_slots, M, N], every slot written, sum over slots
  * = product; n_slots must equal tr_partial_slots or be a valid explicit split) is non-null.
  * When out is used and tr_gemm_workspace_bytes(N, K, M) > 0, `workspace` must hold that many
- * bytes: 64 KiB of int32 counters at offset 0, zero-filled before first use (every call leaves
+ * bytes: 512 KiB of int32 counters (one per 128-byte line) at offset 0, zero-filled before first use (every call leaves
  * them at zero again; no call writes anything else there), then fp32 partials. One buffer
  * sized for the largest call serves every shape; calls that overlap on one device must not
  * share a workspace. N % 16 == 0, K % 128 == 0,

@@ -27,6 +27,8 @@ namespace tr {
 constexpr int kCand = 64;          // sampling candidates (tokenrush/sample.py:12)
 constexpr int kTopChunk = 4096;    // elements per workgroup in the argmax / top-64 kernels
 constexpr int kRun = 16, kChunk = 1024;
+constexpr int kMaxChunks = 256;    // 1024-element chunks per row: V <= 262144
+constexpr int kCntStride = 64;     // ints between workspace counters (one 256-byte line each)
 
 template <typename T>
 __device__ __forceinline__ void ws_st(T* p, T v) {
@@ -51,6 +53,21 @@ __device__ __forceinline__ bool arrive_last(int* cnt, int total) {
   }
   __syncthreads();
   return flag;
+}
+
+// All threads of the block copy n workspace values into LDS with independent agent-scope loads
+// (a serial chain of such loads would cost a memory round trip each).
+template <typename T>
+__device__ __forceinline__ void ws_gather(const T* src, int n, T* dst) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = ws_ld(src + i);
+  __syncthreads();
+}
+
+// Sequential fp32 sum of n LDS values (one thread; fixed left-to-right order).
+__device__ __forceinline__ float seq_sum(const float* v, int n) {
+  float s = 0.f;
+  for (int i = 0; i < n; ++i) s = __fadd_rn(s, v[i]);
+  return s;
 }
 
 // bf16 bits -> unsigned key increasing with the value.
@@ -238,11 +255,12 @@ __device__ void finish_chain(const int64_t* pred, const int64_t* spec, int M, co
 // Longest accepted root path of a draft tree (bench/tree_accept.py:91-100): node 0 is the
 // root; node i > 0 (parent[i] < i) is accepted when its token equals the prediction of its
 // parent's row and the parent is accepted. Deepest accepted node wins, lowest index on ties.
+// Runs on one thread with its node arrays in LDS (no scratch, no registers held by the
+// chunk-scanning part of the kernel).
 __device__ void finish_tree(const int64_t* pred, const int64_t* node_tok, const int32_t* parent, int M,
-                            const AcceptOut& o) {
-  bool ok[32];
-  int depth[32];
-  ok[0] = true;
+                                         const AcceptOut& o) {
+  __shared__ int ok[32], depth[32], path[32];
+  ok[0] = 1;
   depth[0] = 0;
   int best = 0;
   for (int i = 1; i < M; ++i) {
@@ -253,7 +271,6 @@ __device__ void finish_tree(const int64_t* pred, const int64_t* node_tok, const 
     if (ok[i] && depth[i] > depth[best]) best = i;
   }
   const int n = depth[best];
-  int path[32];
   for (int j = best, d = n; d >= 0; --d) {
     path[d] = j;
     j = d > 0 ? parent[j] : 0;
@@ -292,9 +309,26 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
   const int beg = ch * kTopChunk;
   const uint16_t* lg = a.logits + (size_t)row * a.V;
   uint64_t best = 0;
-  for (int i = beg + threadIdx.x; i < min(a.V, beg + kTopChunk); i += blockDim.x) {
-    const uint64_t k = vkey(ord16(lg[i]), i);
-    best = k > best ? k : best;
+  if ((a.V & 7) == 0) {
+    // 16-byte loads: thread t reads elements beg + 8 t + 2048 h + (0..7), h = 0, 1
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i0 = beg + h * (kTopChunk / 2) + threadIdx.x * 8;
+      if (i0 < a.V) {
+        const uint4 v = *(const uint4*)(lg + i0);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint64_t k = vkey(ord16((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), i0 + e);
+          best = k > best ? k : best;
+        }
+      }
+    }
+  } else {
+    for (int i = beg + threadIdx.x; i < min(a.V, beg + kTopChunk); i += blockDim.x) {
+      const uint64_t k = vkey(ord16(lg[i]), i);
+      best = k > best ? k : best;
+    }
   }
   best = wave_max_u64(best);
   __shared__ uint64_t wmax[4];
@@ -304,7 +338,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
     for (int w = 1; w < 4; ++w) best = wmax[w] > best ? wmax[w] : best;
     ws_st(a.keys + blockIdx.x, best);
   }
-  if (!arrive_last(a.cnt_rows + row, a.nch)) return;
+  if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
   if (threadIdx.x < 64) {
     uint64_t b = 0;
     for (int c = threadIdx.x; c < a.nch; c += 64) {
@@ -320,13 +354,19 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
     }
   }
   if (!arrive_last(a.cnt_all, a.M)) return;
-  if (threadIdx.x == 0 && a.fin != FIN_NONE) {
-    int64_t pred[32];
-    for (int i = 0; i < a.M; ++i) pred[i] = ws_ld(a.preds + i);
+  if (a.fin == FIN_NONE) return;
+  __shared__ int64_t pred[32], spec[32];
+  __shared__ int32_t parent[32];
+  if (threadIdx.x < a.M) {
+    spec[threadIdx.x] = a.spec[threadIdx.x];
+    if (a.fin == FIN_TREE) parent[threadIdx.x] = a.parent[threadIdx.x];
+  }
+  ws_gather(a.preds, a.M, pred);
+  if (threadIdx.x == 0) {
     if (a.fin == FIN_CHAIN)
-      finish_chain(pred, a.spec, a.M, a.o);
+      finish_chain(pred, spec, a.M, a.o);
     else
-      finish_tree(pred, a.spec, a.parent, a.M, a.o);
+      finish_tree(pred, spec, parent, a.M, a.o);
   }
 }
 
@@ -348,31 +388,47 @@ struct SampleArgs {
   AcceptOut o;
 };
 
-// One row's pick from its sorted top-64 (value desc, index asc), by lane 0; sequential fp32
-// arithmetic as the file comment states.
+// One row's pick from its sorted top-64 (value desc, index asc), by wave 0: elementwise steps
+// on lane i = rank i, the three running sums sequentially on lane 0 (rank order), as the file
+// comment states. Returns the token in every lane of wave 0.
 __device__ int64_t sample_pick(const uint32_t* tk, const uint32_t* ti, float T, float top_p, int64_t top_k, float u) {
-  const int64_t greedy = ti[0];
-  if (!(T > 0.f)) return greedy;
+  __shared__ float sv[kCand], sp[kCand], scum[kCand];
+  __shared__ float sZ, sTarget;
+  const int i = threadIdx.x;  // 0..63
+  if (!(T > 0.f)) return ti[0];
   const float temp = T > __uint_as_float(0x358637BDu) ? T : __uint_as_float(0x358637BDu);
-  float v[kCand], p[kCand];
-  for (int i = 0; i < kCand; ++i) v[i] = __fdiv_rn(bf16_bits_to_f32(unord16(tk[i])), temp);
-  float Z = 0.f;
-  for (int i = 0; i < kCand; ++i) {
-    p[i] = texp(__fsub_rn(v[i], v[0]));
-    Z = __fadd_rn(Z, p[i]);
+  sv[i] = __fdiv_rn(bf16_bits_to_f32(unord16(tk[i])), temp);
+  __builtin_amdgcn_wave_barrier();
+  const float e = texp(__fsub_rn(sv[i], sv[0]));
+  sp[i] = e;
+  __builtin_amdgcn_wave_barrier();
+  if (i == 0) sZ = seq_sum(sp, kCand);
+  __builtin_amdgcn_wave_barrier();
+  const float p = __fdiv_rn(e, sZ);
+  sp[i] = p;
+  __builtin_amdgcn_wave_barrier();
+  if (i == 0) {
+    float cum = 0.f;
+    for (int k = 0; k < kCand; ++k) {
+      cum = __fadd_rn(cum, sp[k]);
+      scum[k] = cum;
+    }
   }
-  float cum = 0.f, cum2 = 0.f;
-  for (int i = 0; i < kCand; ++i) {
-    p[i] = __fdiv_rn(p[i], Z);
-    cum = __fadd_rn(cum, p[i]);
-    const bool keep = __fsub_rn(cum, p[i]) < top_p && i < top_k;
-    if (!keep) p[i] = 0.f;
-    cum2 = __fadd_rn(cum2, p[i]);
-    v[i] = cum2;  // reuse: running sums of the kept mass
+  __builtin_amdgcn_wave_barrier();
+  const bool keep = __fsub_rn(scum[i], p) < top_p && i < top_k;
+  sp[i] = keep ? p : 0.f;
+  __builtin_amdgcn_wave_barrier();
+  if (i == 0) {
+    float cum2 = 0.f;
+    for (int k = 0; k < kCand; ++k) {
+      cum2 = __fadd_rn(cum2, sp[k]);
+      scum[k] = cum2;
+    }
+    sTarget = __fmul_rn(u, cum2);
   }
-  const float target = __fmul_rn(u, cum2);
-  int pick = 0;
-  for (int i = 0; i < kCand; ++i) pick += v[i] < target;
+  __builtin_amdgcn_wave_barrier();
+  const unsigned long long below = __ballot(scum[i] < sTarget);
+  int pick = __popcll(below);
   if (pick > kCand - 1) pick = kCand - 1;
   return ti[pick];
 }
@@ -384,11 +440,25 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   const int beg = ch * kTopChunk;
   const uint16_t* lg = a.logits + (size_t)row * a.V;
   uint32_t k16[E], idx[E];
+  const int i0 = beg + threadIdx.x * E;
+  if ((a.V & 7) == 0 && i0 + E <= a.V) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int i = beg + threadIdx.x * E + e;
-    idx[e] = i;
-    k16[e] = i < a.V ? ord16(lg[i]) : 0u;
+    for (int h = 0; h < E / 8; ++h) {
+      const uint4 v = *(const uint4*)(lg + i0 + 8 * h);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        idx[8 * h + e] = i0 + 8 * h + e;
+        k16[8 * h + e] = ord16((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = i0 + e;
+      idx[e] = i;
+      k16[e] = i < a.V ? ord16(lg[i]) : 0u;
+    }
   }
   select_top64<E>(k16, idx, tk, ti);
   uint32_t* mine = a.cand + ((size_t)row * a.nch + ch) * kCand * 2;
@@ -396,7 +466,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     ws_st(mine + 2 * threadIdx.x, tk[threadIdx.x]);
     ws_st(mine + 2 * threadIdx.x + 1, ti[threadIdx.x]);
   }
-  if (!arrive_last(a.cnt_rows + row, a.nch)) return;
+  if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
   // merge: the nch sorted lists in chunk order keep equal values in index order
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -411,19 +481,20 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     }
   }
   select_top64<E>(k16, idx, tk, ti);
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 64) {
     const int64_t t = sample_pick(tk, ti, *a.temperature, *a.top_p, *a.top_k, a.u[row]);
-    if (a.out) a.out[row] = t;
-    ws_st(a.preds + row, t);
+    if (threadIdx.x == 0) {
+      if (a.out) a.out[row] = t;
+      ws_st(a.preds + row, t);
+    }
   }
   if (!arrive_last(a.cnt_all, a.M)) return;
-  if (threadIdx.x == 0 && a.fin == FIN_CHAIN) {
-    int64_t pred[32];
-    for (int i = 0; i < a.M; ++i) pred[i] = ws_ld(a.preds + i);
-    if (a.o.pred)
-      for (int i = 0; i < a.M; ++i) a.o.pred[i] = pred[i];
-    finish_chain(pred, a.spec, a.M, a.o);
-  }
+  if (a.fin != FIN_CHAIN) return;
+  __shared__ int64_t pred[32], spec[32];
+  if (threadIdx.x < a.M) spec[threadIdx.x] = a.spec[threadIdx.x];
+  ws_gather(a.preds, a.M, pred);
+  if (a.o.pred && threadIdx.x < a.M) a.o.pred[threadIdx.x] = pred[threadIdx.x];
+  if (threadIdx.x == 0) finish_chain(pred, spec, a.M, a.o);
 }
 
 // ------------------------------------------------------------------ residual rejection sampling
@@ -451,16 +522,44 @@ struct ResidualArgs {
 template <int MODE>  // 0: e, 1: residual, 2: p
 __device__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float Zr, float (&vals)[kRun]) {
   const uint16_t* lg = a.logits + (size_t)row * a.V;
+  const float* qr = a.q + (size_t)row * a.V;
+  const int i0 = ch * kChunk + lane * kRun;
+  uint32_t lb[kRun];
+  float qv[kRun];
+  if ((a.V & 7) == 0 && i0 + kRun <= a.V) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint4 v = *(const uint4*)(lg + i0 + 8 * h);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lb[8 * h + e] = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+    }
+    if (MODE == 1) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float4 v = *(const float4*)(qr + i0 + 4 * h);
+        qv[4 * h] = v.x;
+        qv[4 * h + 1] = v.y;
+        qv[4 * h + 2] = v.z;
+        qv[4 * h + 3] = v.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kRun; ++e) {
+      lb[e] = i0 + e < a.V ? lg[i0 + e] : 0u;
+      if (MODE == 1) qv[e] = i0 + e < a.V ? qr[i0 + e] : 0.f;
+    }
+  }
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < kRun; ++e) {
-    const int i = ch * kChunk + lane * kRun + e;
     float v = 0.f;
-    if (i < a.V) {
-      v = texp(__fsub_rn(bf16_bits_to_f32(lg[i]), mx));
+    if (i0 + e < a.V) {
+      v = texp(__fsub_rn(bf16_bits_to_f32(lb[e]), mx));
       if (MODE >= 1) v = __fdiv_rn(v, Zr);
       if (MODE == 1) {
-        v = __fsub_rn(v, a.q[(size_t)row * a.V + i]);
+        v = __fsub_rn(v, qv[e]);
         v = v > 0.f ? v : 0.f;
       }
     }
@@ -496,24 +595,24 @@ __global__ __launch_bounds__(64) void residual_phase2_kernel(ResidualArgs a) {
     if (d >= base && d < base + kRun) ws_st(a.e_draft + row, vals[d - base]);
   }
   if (lane == 0) ws_st(a.chunk_sum + blockIdx.x, ct);
-  if (!arrive_last(a.cnt_rows + row, a.nch)) return;
-  if (lane == 0) {
-    float z = 0.f;
-    for (int c = 0; c < a.nch; ++c) z = __fadd_rn(z, ws_ld(a.chunk_sum + (size_t)row * a.nch + c));
-    ws_st(a.Z + row, z);
-  }
+  if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
+  __shared__ float cs[kMaxChunks];
+  ws_gather(a.chunk_sum + (size_t)row * a.nch, a.nch, cs);
+  if (lane == 0) ws_st(a.Z + row, seq_sum(cs, a.nch));
   if (!arrive_last(a.cnt_all, a.M)) return;
+  __shared__ float ed[32], zz[32], qd[32];
+  __shared__ int dvalid[32];
+  ws_gather(a.e_draft, K, ed);
+  ws_gather(a.Z, K, zz);
+  if (lane < K) {
+    const int64_t d = a.spec[lane + 1];
+    dvalid[lane] = d >= 0 && d < a.V;  // an out-of-vocabulary draft is rejected
+    qd[lane] = dvalid[lane] ? a.q[(size_t)lane * a.V + d] : 0.f;
+  }
+  __syncthreads();
   if (lane == 0) {
     int n = 0;
-    while (n < K) {
-      const int64_t d = a.spec[n + 1];
-      if (d < 0 || d >= a.V) break;  // an out-of-vocabulary draft is rejected
-      const float pd = __fdiv_rn(ws_ld(a.e_draft + n), ws_ld(a.Z + n));
-      if (__fmul_rn(a.u[n], a.q[(size_t)n * a.V + d]) < pd)
-        ++n;
-      else
-        break;
-    }
+    while (n < K && dvalid[n] && __fmul_rn(a.u[n], qd[n]) < __fdiv_rn(ed[n], zz[n])) ++n;
     ws_st(a.n_ws, n);
   }
 }
@@ -536,16 +635,17 @@ __global__ __launch_bounds__(64) void residual_phase3_kernel(ResidualArgs a) {
   __shared__ float s_acc;
   __shared__ float s_target;
   __shared__ int s_degenerate;
+  __shared__ float cs[kMaxChunks];
+  ws_gather(a.chunk_sum, a.nch, cs);
   if (lane == 0) {
-    float R = 0.f;
-    for (int c = 0; c < a.nch; ++c) R = __fadd_rn(R, ws_ld(a.chunk_sum + c));
+    const float R = seq_sum(cs, a.nch);
     s_degenerate = !(R > 0.f);
     const float target = __fmul_rn(a.u[K], R);
     // first chunk whose running total exceeds the target; else the last nonzero chunk
     float cp = 0.f, cp_last = 0.f;
     int c_found = -1, c_last = -1;
     for (int c = 0; c < a.nch; ++c) {
-      const float t = ws_ld(a.chunk_sum + c);
+      const float t = cs[c];
       if (t > 0.f) {
         c_last = c;
         cp_last = cp;
@@ -619,7 +719,7 @@ __global__ __launch_bounds__(64) void residual_phase3_kernel(ResidualArgs a) {
       }
       pick = (int)vkey_idx(b);
     }
-    const int n = j;
+    const int n = j;  // drafts a.spec[1..n] were accepted
     const int64_t base = *a.o.pos;
     *a.o.n_accepted = n;
     *a.o.tok = pick;
@@ -668,9 +768,10 @@ using namespace tr;
 
 namespace {
 
-// Workspace layout (bytes): [0, 4096) int32 counters (zero between calls);
-// then the largest of the per-kernel scratch areas.
-constexpr size_t kCntBytes = 4096;
+// Workspace layout (bytes): [0, kCntBytes) int32 counters (zero between calls), one per
+// 256-byte line so that atomics on different counters never share a cache line (agent-scope
+// atomics on one line serialize); then the largest of the per-kernel scratch areas.
+constexpr size_t kCntBytes = 160 * kCntStride * sizeof(int);
 
 int nch_top(int V) { return (V + kTopChunk - 1) / kTopChunk; }
 int nch_run(int V) { return (V + kChunk - 1) / kChunk; }
@@ -691,7 +792,7 @@ struct WsView {
 
 bool ws_view(void* ws, size_t bytes, int M, int V, WsView* v) {
   if (!ws || bytes < kCntBytes + scratch_bytes(M, V)) return false;
-  v->cnt = (int*)ws;
+  v->cnt = (int*)ws;  // counter c lives at cnt[c * kCntStride]
   v->scratch = (char*)ws + kCntBytes;
   return true;
 }
@@ -711,8 +812,8 @@ AcceptOut make_out(int64_t* pred, int64_t* n, int64_t* tok, int64_t* pos, int64_
   return o;
 }
 
-// counters: [0, 32) rows of the first kernel, [32] all-rows of the first kernel,
-// [64, 96) rows of the residual phase 2, [96] its all-rows, [128] phase 3.
+// counters (in units of kCntStride ints): [0, 32) rows of the first kernel, [32] all-rows of
+// the first kernel, [64, 96) rows of the residual phase 2, [96] its all-rows, [128] phase 3.
 int launch_argmax(const void* logits, int M, int V, int fin, const int64_t* spec, const int32_t* parent,
                   const WsView& w, float* rowmax, const AcceptOut& o, hipStream_t st) {
   ArgmaxArgs a;
@@ -727,7 +828,7 @@ int launch_argmax(const void* logits, int M, int V, int fin, const int64_t* spec
   a.preds = (int64_t*)(w.scratch + (size_t)M * a.nch * 8);
   a.rowmax = rowmax;
   a.cnt_rows = w.cnt;
-  a.cnt_all = w.cnt + 32;
+  a.cnt_all = w.cnt + 32 * kCntStride;
   a.o = o;
   hipLaunchKernelGGL(argmax_kernel, dim3(M * a.nch), dim3(256), 0, st, a);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
@@ -794,7 +895,7 @@ static int launch_sample(const void* logits, int M, int V, int fin, const float*
   a.cand = (uint32_t*)w.scratch;
   a.preds = (int64_t*)(w.scratch + (size_t)M * a.nch * kCand * 8);
   a.cnt_rows = w.cnt;
-  a.cnt_all = w.cnt + 32;
+  a.cnt_all = w.cnt + 32 * kCntStride;
   a.out = out;
   a.o = o;
   hipLaunchKernelGGL(sample_kernel, dim3(M * a.nch), dim3(256), 0, st, a);
@@ -847,12 +948,12 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
   a.Z = (float*)r;
   a.e_draft = a.Z + M;
   a.n_ws = (int*)(a.e_draft + M);
-  a.cnt_rows = w.cnt + 64;
-  a.cnt_all = w.cnt + 96;
+  a.cnt_rows = w.cnt + 64 * kCntStride;
+  a.cnt_all = w.cnt + 96 * kCntStride;
   a.o = make_out(nullptr, n_accepted, tok, pos, slot, tokens, commit);
   hipLaunchKernelGGL(residual_phase2_kernel, dim3(M * a.nch), dim3(64), 0, st, a);
   if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
-  a.cnt_all = w.cnt + 128;
+  a.cnt_all = w.cnt + 128 * kCntStride;
   hipLaunchKernelGGL(residual_phase3_kernel, dim3(a.nch), dim3(64), 0, st, a);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }

@@ -41,6 +41,8 @@ namespace tr {
 
 constexpr int kGroup = 128;
 constexpr int kTileBytes = 1088;
+constexpr int kWsCounterStride = 32;  // ints between workspace counters: one per 128-byte line
+                                      // (agent-scope atomics on one line serialize)
 constexpr int kMaxWaves = 12;   // 768 threads: leaves ~170 VGPRs per lane (3 waves per SIMD)
 
 enum { OUT_BF16 = 0, OUT_PARTIAL = 1, OUT_BF16_VIA_WS = 2 };
@@ -233,7 +235,8 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(a.ws_cnt + rbi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.S - 1;
+    last = __hip_atomic_fetch_add(a.ws_cnt + rbi * kWsCounterStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           a.S - 1;
   __syncthreads();
   if (!last) return;
   const int cols = (r1 - r0) * 16;
@@ -244,7 +247,8 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
       v += __hip_atomic_load(a.ws_part + ((size_t)s * a.M + m) * a.N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
   }
-  if (threadIdx.x == 0) __hip_atomic_store(a.ws_cnt + rbi, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.ws_cnt + rbi * kWsCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------------------- layout kernels
@@ -424,8 +428,8 @@ int tr_partial_slots(int N, int K, int M) {
 // Workspace of an out-mode call with S > 1: kWsCounters int32 counters at offset 0 -- a fixed
 // region no call ever uses for partials, so one zero-filled buffer serves calls of every shape
 // -- then the fp32 partials [S, M, N].
-constexpr int kWsCounters = 16384;
-static size_t ws_counter_bytes() { return (size_t)kWsCounters * sizeof(int); }
+constexpr int kWsCounters = 4096;
+static size_t ws_counter_bytes() { return (size_t)kWsCounters * kWsCounterStride * sizeof(int); }
 
 size_t tr_gemm_workspace_bytes(int N, int K, int M) {
   Plan p;

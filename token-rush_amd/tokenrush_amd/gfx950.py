@@ -28,6 +28,7 @@ GROUP = 128
 TILE = 1088
 MAX_ROWS = 32        # two 16-row MFMA tiles
 SCALE_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
+WS_COUNTER_BYTES = 4096 * 128   # the workspace's counter region (one counter per 128-byte line)
 
 
 def ext():
@@ -129,7 +130,7 @@ def _launch(x, B, s, y, partial, n_slots, strips_per_wg=-1, slots=0):
         raise RuntimeError(f"problem shape (m={M}, n={N}, k={K}) not supported: need m <= {MAX_ROWS}")
     _lib.require_gpu(x, B, y)
     ws, nbytes = None, 0
-    need = workspace_bytes(N, K, M) if slots == 0 else (65536 + 4 * slots * M * N if slots > 1 else 0)
+    need = workspace_bytes(N, K, M) if slots == 0 else (WS_COUNTER_BYTES + 4 * slots * M * N if slots > 1 else 0)
     if not partial and need > 0:
         ws, nbytes = workspaces(N, x.device, K, M, min_bytes=need)
         if nbytes < need:
