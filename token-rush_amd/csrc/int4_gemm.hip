@@ -31,7 +31,7 @@
 // Work split ("activation-stationary"): a workgroup owns a range of strips and a K slot; each
 // of its W waves owns one K block of GW groups (GW = 4 for M <= 16, 2 above), loads that
 // block's activations into registers once, then streams the strips' tiles for its block.
-// After each strip the waves' partial tiles are summed through LDS in fixed wave order
+// After every few strips the waves' partial tiles are summed through LDS in fixed wave order
 // (deterministic). With S > 1 slots, slots write fp32 partials: either the caller's
 // [S, M, N] buffer (the contract of the reference's partials(), tokenrush/quant.py:381-391,
 // tokenrush/marlin.py:158-168) or a workspace the last-arriving slot reduces into bf16.
@@ -52,11 +52,15 @@ struct Tile {
   uint32_t sm;   // scale | min << 16 of row lane % 16
 };
 
-__device__ __forceinline__ void load_tile(Tile& t, const uint8_t* __restrict__ tile, int lane) {
+// Tile loads go through a buffer resource: the tile's byte offset is wave-uniform (an SGPR)
+// and the lane offsets are loop-invariant VGPRs, so no vector instruction computes addresses.
+// nt (non-temporal): the weights are streamed once. Reads past the resource size return 0.
+__device__ __forceinline__ void load_tile(Tile& t, __amdgpu_buffer_rsrc_t rsrc, int tile_off, int lane_off,
+                                          int sm_off) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = __builtin_nontemporal_load((const u32x4*)(tile + 16 * lane));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off, tile_off, 2 /* nt */);
   t.w = make_uint4(v.x, v.y, v.z, v.w);
-  t.sm = __builtin_nontemporal_load((const uint32_t*)(tile + 1024 + 4 * (lane & 15)));
+  t.sm = __builtin_amdgcn_raw_buffer_load_b32(rsrc, sm_off, tile_off, 2 /* nt */);
 }
 
 // E = sum over the group of x * (128 + q), then acc += s * E + (mn - 128 s) * X.
@@ -105,6 +109,7 @@ struct GemmArgs {
   float* ws_part;         // fp32 [S, M, N] workspace (OUT_BF16_VIA_WS)
   int* ws_cnt;            // one counter per workgroup row range (<= N/16), zero between calls
   int M, N, K, S, R;      // R = strips per workgroup
+  int RB;                 // strips per LDS reduction batch
   int mode;
 };
 
@@ -135,11 +140,14 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 
   // Tile pointer of (strip r, group gbase + gw); clamped so that loads past the end re-read a
   // valid tile (keeps every loop path's load count equal; those values are never used).
-  auto tile_ptr = [&](int r, int gw) {
+  auto tile_off = [&](int r, int gw) {
     const int rr = min(r, r1 - 1);
     const int g = gbase + min(gw, ng - 1);
-    return a.packed + ((size_t)rr * G + g) * kTileBytes;
+    return __builtin_amdgcn_readfirstlane((rr * G + g) * kTileBytes);
   };
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.packed, (short)0, (int)((size_t)nstrips * G * kTileBytes), 0x00020000);
+  const int lane_off = 16 * lane, sm_off = 1024 + 4 * (lane & 15);
 
   // Activations of this wave's K block, in registers for the whole strip loop.
   uint4 xa[GW][MT][4];
@@ -165,7 +173,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int gw = 0; gw < GW; ++gw) load_tile(buf[h][gw], tile_ptr(r0 + h, gw), lane);
+      for (int gw = 0; gw < GW; ++gw) load_tile(buf[h][gw], rsrc, tile_off(r0 + h, gw), lane_off, sm_off);
   }
 
   {
@@ -183,6 +191,10 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
       }
   }
 
+  // Partial tiles of RB consecutive strips are collected in LDS and reduced together (one
+  // barrier per batch); batches alternate between two halves of the LDS ring, so the next
+  // batch's writes never race the previous batch's reads.
+  const int RB = a.RB;
   for (int rb = r0; rb < r1; rb += 2) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -195,33 +207,41 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 #pragma unroll
           for (int gw = 0; gw < GW; ++gw) {
             if (gw < ng) tile_mac<MT, F16S>(buf[h][gw], xa[gw], X[gw], acc, kExp128);
-            load_tile(buf[h][gw], tile_ptr(r + 2, gw), lane);
+            load_tile(buf[h][gw], rsrc, tile_off(r + 2, gw), lane_off, sm_off);
           }
         }
-        // This wave's partial of strip r -> LDS (ring of 2), then the workgroup reduces it.
-        float* mine = red + (((size_t)(r & 1) * W + wave) * MT) * 256;
+        const int sib = (r - r0) % RB, half = ((r - r0) / RB) & 1;
+        float* ring = red + (size_t)half * RB * W * MT * 256;
         if (active) {
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) *(f32x4*)(mine + mt * 256 + lane * 4) = acc[mt];
+          for (int mt = 0; mt < MT; ++mt)
+            *(f32x4*)(ring + ((size_t)(sib * W + wave) * MT + mt) * 256 + lane * 4) = acc[mt];
         }
-        __syncthreads();
-        const float* ring = red + (size_t)(r & 1) * W * MT * 256;
-        for (int e = threadIdx.x; e < MT * 256; e += blockDim.x) {
-          const int mt = e >> 8, l = (e >> 2) & 63, rr = e & 3;
-          const int m = 16 * mt + 4 * (l >> 4) + rr;
-          if (m >= a.M) continue;
-          float v = 0.f;
-          for (int w = 0; w < nw; ++w) v += ring[w * MT * 256 + e];
-          const int n = 16 * r + (l & 15);
-          if (a.mode == OUT_BF16)
-            ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
-          else if (a.mode == OUT_PARTIAL)
-            ((float*)a.out)[((size_t)slot * a.M + m) * a.N + n] = v;
-          else  // agent-scope store: written through to the coherence point, no L2 flush needed
-            __hip_atomic_store(a.ws_part + ((size_t)slot * a.M + m) * a.N + n, v, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        if (sib == RB - 1 || r == r1 - 1) {
+          __syncthreads();
+          const int ns = sib + 1, r_first = r - sib, per = a.M * 16;
+          for (int e = threadIdx.x; e < ns * per; e += blockDim.x) {
+            const int sidx = e / per, rem = e % per;
+            const int m = rem >> 4, n16 = rem & 15;
+            const int mt = m >> 4, mm = m & 15;
+            const float* src = ring + ((size_t)sidx * W * MT + mt) * 256 + (16 * (mm >> 2) + n16) * 4 + (mm & 3);
+            float part[kMaxWaves];
+#pragma unroll
+            for (int w = 0; w < kMaxWaves; ++w) part[w] = w < nw ? src[(size_t)w * MT * 256] : 0.f;
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < kMaxWaves; ++w)
+              if (w < nw) v += part[w];
+            const int n = 16 * (r_first + sidx) + n16;
+            if (a.mode == OUT_BF16)
+              ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
+            else if (a.mode == OUT_PARTIAL)
+              ((float*)a.out)[((size_t)slot * a.M + m) * a.N + n] = v;
+            else  // agent-scope store: written through to the coherence point, no L2 flush needed
+              __hip_atomic_store(a.ws_part + ((size_t)slot * a.M + m) * a.N + n, v, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
-        // The next write to this ring half is two strips later, after the next barrier.
       }
     }
   }
@@ -357,6 +377,7 @@ namespace {
 
 constexpr int kCUs = 256;          // MI355X compute units
 constexpr int kWavesPerCU = 12;    // occupancy of the GEMM kernel (about 150 VGPRs per lane)
+constexpr size_t kLdsBudget = 64 * 1024;  // dynamic LDS of one workgroup (the default limit)
 
 struct Plan {
   int GW, S, W, R, grid_n;
@@ -392,14 +413,16 @@ bool make_plan(int N, int K, int M, int S_req, int R_req, Plan* p) {
 }
 
 template <int MT, int GW, bool F16S>
-hipError_t launch_t(const GemmArgs& a, const Plan& p, hipStream_t stream) {
+hipError_t launch_t(GemmArgs a, const Plan& p, hipStream_t stream) {
   const dim3 grid(p.grid_n * p.S), block(64 * p.W);
-  const size_t lds = (size_t)2 * p.W * MT * 256 * sizeof(float);
-  hipLaunchKernelGGL((int4_gemm_kernel<MT, GW, F16S>), grid, block, lds, stream, a);
+  const size_t per_strip = (size_t)p.W * MT * 256 * sizeof(float);
+  int rb = (int)(kLdsBudget / (2 * per_strip));
+  a.RB = rb < 1 ? 1 : (rb > 4 ? 4 : rb);
+  hipLaunchKernelGGL((int4_gemm_kernel<MT, GW, F16S>), grid, block, 2 * a.RB * per_strip, stream, a);
   return hipGetLastError();
 }
 
-hipError_t launch(const GemmArgs& a, const Plan& p, int scale_dtype, hipStream_t stream) {
+hipError_t launch(const GemmArgs& a, const Plan& p, int scale_dtype, hipStream_t stream) {  // NOLINT
   const bool f16 = scale_dtype == 1;
   if (a.M > 16) return f16 ? launch_t<2, 2, true>(a, p, stream) : launch_t<2, 2, false>(a, p, stream);
   return f16 ? launch_t<1, 4, true>(a, p, stream) : launch_t<1, 4, false>(a, p, stream);
