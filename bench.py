@@ -17,8 +17,9 @@ roofline    the dominant kernel (gate/up, 53% of the bytes): its algorithmic byt
             kernel alone over all weight copies, on the launch stream; vs 8 TB/s.
 accept      on-device accept latency (BASELINE config 3 and 4): mean per launch over a graph of
             back-to-back calls.
-cpu_baseline  the CPU oracle (numpy dequantize + matmul: the reference's torch path restated)
-            on one layer set at M = 8, one thread, on this host.
+cpu_baseline  the reference's CPU path restated in torch (unpack, in-place dequant, F.linear) on
+            one layer set at M = 8, OMP_NUM_THREADS host cores, median of >= 5 passes
+            (about 10 s).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -139,32 +140,36 @@ def accept_latency(torch, dev):
     return res
 
 
-def cpu_baseline(M=M_VERIFY):
-    """Oracle (numpy, single thread) dequantize + matmul over one layer set at M rows."""
-    import numpy as np  # noqa: F401
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:     # pragma: no cover
-        threadpool_limits = None
+def cpu_baseline(M=M_VERIFY, min_reps=5, budget_s=10.0):
+    """The reference's CPU path restated (oracle.int4.torch_dequant_linear: torch unpack, in-place
+    fp16 dequant, F.linear in bf16) over one layer set at M rows on the host's CPU share; median of
+    the timed passes (at least `min_reps`, then until `budget_s` seconds) after one warm-up pass."""
+    import numpy as np
+    import torch
     sys.path.insert(0, ROOT)
     from oracle import int4 as o
-    total_bytes, total_s = 0, 0.0
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    try:
-        for i, (name, N, K, partial) in enumerate(LAYER_SET):
-            p, s, m = o.make_weights(N, K, seed=300 + i, dtype="fp16")
-            x = o.make_x(M, K, seed=400 + i)
-            t0 = time.perf_counter()
-            y = o.gemm_dequant(x, p, s, m, "fp16")
-            total_s += time.perf_counter() - t0
-            total_bytes += algo_bytes(N, K, M)
-            del p, s, m, y
-    finally:
-        if ctx is not None:
-            ctx.__exit__(None, None, None)
-    return {"value": round(total_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"one config-2 layer set (4 projections, 178 MB of int4 weights) at M={M}: numpy "
-                      f"dequantize (two fp16 roundings) + fp64 matmul, {total_s:.1f} s"}
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)   # the host's CPU share
+    torch.set_num_threads(cores)
+    layers = []
+    for i, (name, N, K, partial) in enumerate(LAYER_SET):
+        p, s, m = o.make_weights(N, K, seed=300 + i, dtype="fp16")
+        x = o.make_x(M, K, seed=400 + i)
+        layers.append((torch.from_numpy(x).to(torch.bfloat16), torch.from_numpy(p),
+                       torch.from_numpy(s).half(), torch.from_numpy(m).half(), algo_bytes(N, K, M)))
+    total_bytes = sum(L[-1] for L in layers)
+    times, r = [], 0
+    while r <= min_reps or sum(times) < budget_s:
+        t0 = time.perf_counter()
+        for x, p, s, m, _ in layers:
+            o.torch_dequant_linear(x, p, s, m)
+        if r:
+            times.append(time.perf_counter() - t0)
+        r += 1
+    t = float(np.median(times))
+    return {"value": round(total_bytes / t / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"one config-2 layer set (4 projections, 178 MB int4 weights) at M={M}: torch CPU "
+                      f"unpack + in-place fp16 dequant + bf16 F.linear on {cores} threads, median of {len(times)} "
+                      f"passes ({t * 1e3:.0f} ms each, {sum(times):.1f} s timed)"}
 
 
 def main():

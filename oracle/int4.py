@@ -13,6 +13,8 @@ Pinning:
                                     on weights built from codes.
   gemm_exact / gemm_dequant      -- brute-force triple loop on tiny shapes; fp64 matmul.
   gemm_fold                      -- equals gemm_exact within fp32 error (algebraic identity).
+  torch_dequant_linear           -- equals gemm_dequant within bf16 output rounding plus a bf16
+                                    matmul's accumulation error (the same dequantized weights).
   pack_strip                     -- our own layout (not the reference's): its definition is
                                     checked by a per-element brute force and by unpack_strip.
 """
@@ -194,3 +196,17 @@ def make_x(M: int, K: int, seed: int) -> np.ndarray:
     """bf16-valued activations ~N(0, 1)."""
     rng = np.random.default_rng(seed)
     return bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+
+
+def torch_dequant_linear(x, packed, scale, mn):
+    """The reference's `dequant` backend as torch runs it on the CPU: unpack, one bf16 (or fp16)
+    temporary multiplied and added in place, then F.linear in that dtype (tokenrush/quant.py:39-53,
+    quant.py:373-374). Arguments are torch CPU tensors: x [M, K] bf16, packed uint8 [N, K/2],
+    scale / mn [N, K/128] in the parameter dtype. Returns [M, N] in x's dtype. Used as the CPU
+    baseline's timed body and checked against gemm_dequant."""
+    import torch
+    import torch.nn.functional as F
+    N, G = scale.shape
+    w = torch.stack([packed & 0xF, packed >> 4], dim=-1).view(N, -1).to(scale.dtype).view(N, G, -1)
+    w.mul_(scale[..., None]).add_(mn[..., None])
+    return F.linear(x, w.view(N, -1).to(x.dtype))

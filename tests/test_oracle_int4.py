@@ -123,3 +123,14 @@ def test_pack_strip_per_element():
             assert sm & 0xFFFF == int(o.to_bits(s[n, g], "fp16")) and sm >> 16 == int(o.to_bits(m[n, g], "fp16"))
     p2, s2, m2 = o.unpack_strip(st, "fp16")
     assert np.array_equal(p2, p) and np.array_equal(s2, s) and np.array_equal(m2, m)
+
+
+def test_torch_dequant_linear_matches_numpy_path():
+    import torch
+    p, s, m = o.make_weights(256, 1024, seed=77, dtype="bf16")
+    x = o.make_x(4, 1024, seed=78)
+    bf = lambda a: torch.from_numpy(a).to(torch.bfloat16)
+    y = o.torch_dequant_linear(bf(x), torch.from_numpy(p), bf(s), bf(m)).float().numpy()
+    ref = o.gemm_dequant(x, p, s, m, "bf16")
+    assert np.abs(y - ref).max() <= np.abs(ref).max() * 2 ** -7
+    assert np.linalg.norm(y - ref) <= 1e-2 * np.linalg.norm(ref)
