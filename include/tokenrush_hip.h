@@ -13,7 +13,10 @@
  *   x        bf16 [M, K]                 activations (M <= 32)
  *   qweight  uint8 [N, K/2]              engine packing: element 2j in the low nibble of byte j
  *                                        (tokenrush/quant.py:9-10)
- *   packed   uint8 [N/16, K/128, 1088]   strip layout made by tr_pack_int4 (codes + scale/min)
+ *   packed   uint8 [N/16, Gp/4, 4352]    quad layout made by tr_pack_int4: Gp = K/128 rounded up to
+ *                                        a multiple of 4 (zero padding); per 16-row strip and four
+ *                                        groups, 4 x 1024 bytes of codes then 16 rows x 4 groups of
+ *                                        (scale | min << 16) -- tr_packed_bytes(N, K) bytes
  *   scale,mn [N, K/128]                  bf16 (scale_dtype 0, the engine format) or fp16 (1)
  */
 #ifndef TOKENRUSH_HIP_H
@@ -35,7 +38,7 @@ extern "C" {
  * bytes: 512 KiB of int32 counters (one per 128-byte line) at offset 0, zero-filled before first use (every call leaves
  * them at zero again; no call writes anything else there), then fp32 partials. One buffer
  * sized for the largest call serves every shape; calls that overlap on one device must not
- * share a workspace. N % 16 == 0, K % 128 == 0,
+ * share a workspace. N % 16 == 0, K % 128 == 0, tr_packed_bytes(N, K) > 0,
  * group == 128.
  * Replaces: marlin_bf16_cuda (tokenrush/csrc/marlin_bf16.cu:630-670) behind the torch binding
  * `mul(A, B, C, s, m, workspace, red, ...)` (tokenrush/csrc/marlin_bf16.cpp:14-44): C bf16 ->
@@ -64,7 +67,12 @@ int tr_partial_slots(int N, int K, int M);
  * Replaces: the lock + fp32 reduce buffer sizing of marlin.workspaces (tokenrush/marlin.py:121-135). */
 size_t tr_gemm_workspace_bytes(int N, int K, int M);
 
-/* Engine packing + scale/min -> strip layout uint8 [N/16, K/128, 1088], and back.
+/* Bytes of the quad layout of an N x K weight (0: unsupported shape -- N % 16, K % 128, or a
+ * packed size of 2 GiB or more). Host only. */
+size_t tr_packed_bytes(int N, int K);
+
+/* Engine packing + scale/min -> quad layout (tr_packed_bytes(N, K) bytes), and back (padding
+ * groups dropped).
  * Replaces: marlin.pack / marlin.unpack (tokenrush/marlin.py:73-118), torch-op layout
  * conversions in the reference. */
 int tr_pack_int4(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K,

@@ -15,8 +15,8 @@ Pinning:
   gemm_fold                      -- equals gemm_exact within fp32 error (algebraic identity).
   torch_dequant_linear           -- equals gemm_dequant within bf16 output rounding plus a bf16
                                     matmul's accumulation error (the same dequantized weights).
-  pack_strip                     -- our own layout (not the reference's): its definition is
-                                    checked by a per-element brute force and by unpack_strip.
+  pack_quads                     -- our own layout (not the reference's): its definition is
+                                    checked by a per-element brute force and by unpack_quads.
 """
 import numpy as np
 
@@ -76,38 +76,49 @@ def pack_engine(codes: np.ndarray) -> np.ndarray:
 NIBBLE_K = np.array([0, 2, 4, 6, 1, 3, 5, 7])
 
 
-TILE = 1088
+QUAD = 4352          # bytes per (16-row strip, 4 groups) quad
+SM_OFF = 4096        # offset of the quad's (scale, min) words
 
 
-def pack_strip(packed: np.ndarray, scale: np.ndarray, mn: np.ndarray, dtype: str = "bf16") -> np.ndarray:
-    """Engine packing + scale/min -> the gfx950 strip layout uint8 [N/16, G, 1088] (the layout
+def padded_groups(K: int) -> int:
+    """K/128 rounded up to whole quads of four groups."""
+    return -(-(K // GROUP) // 4) * 4
+
+
+def pack_quads(packed: np.ndarray, scale: np.ndarray, mn: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """Engine packing + scale/min -> the gfx950 quad layout uint8 [N/16, Gp/4, 4352] (the layout
     token-rush_amd/csrc/int4_gemm.hip documents; it has no counterpart in the reference, whose
-    load-time repack is Marlin's, marlin.py:73-96): per (strip, group) 1024 bytes of codes in
-    lane order, then 16 x (scale bits | min bits << 16)."""
+    load-time repack is Marlin's, marlin.py:73-96). Groups are padded with zeros to Gp, a
+    multiple of 4. Per (strip, quad): four 1024-byte blocks of codes in lane order, then
+    16 rows x 4 groups of (scale bits | min bits << 16)."""
     codes = unpack_int4(packed).astype(np.uint32)
     N, K = codes.shape
-    S, G = N // 16, K // GROUP
-    a = codes.reshape(S, 16, G, 4, 4, 8)                 # strip, n, g, c, j, kk
-    a = a.transpose(0, 2, 3, 1, 4, 5).reshape(S, G, 64, 4, 8)   # lane = 16 c + n
-    words = np.zeros((S, G, 64, 4), dtype=np.uint32)
+    S, G, Gp = N // 16, K // GROUP, padded_groups(K)
+    c = np.zeros((N, Gp * GROUP), dtype=np.uint32)
+    c[:, :K] = codes
+    a = c.reshape(S, 16, Gp, 4, 4, 8)                    # strip, n, g, c, j, kk
+    a = a.transpose(0, 2, 3, 1, 4, 5).reshape(S, Gp, 64, 4, 8)   # lane = 16 c + n
+    words = np.zeros((S, Gp, 64, 4), dtype=np.uint32)
     for p in range(8):
         words |= a[..., NIBBLE_K[p]] << np.uint32(4 * p)
-    sm = (to_bits(scale, dtype).astype(np.uint32) | (to_bits(mn, dtype).astype(np.uint32) << np.uint32(16)))
-    sm = sm.reshape(S, 16, G).transpose(0, 2, 1)         # [S, G, 16]
-    out = np.concatenate([words.reshape(S, G, 256), sm], axis=-1)
-    return np.ascontiguousarray(out).view(np.uint8).reshape(S, G, TILE)
+    sm = np.zeros((N, Gp), dtype=np.uint32)
+    sm[:, :G] = to_bits(scale, dtype).astype(np.uint32) | (to_bits(mn, dtype).astype(np.uint32) << np.uint32(16))
+    sm = sm.reshape(S, 16, Gp // 4, 4).transpose(0, 2, 1, 3).reshape(S, Gp // 4, 64)   # [S, q, row, t]
+    out = np.concatenate([words.reshape(S, Gp // 4, 1024), sm], axis=-1)
+    return np.ascontiguousarray(out).view(np.uint8).reshape(S, Gp // 4, QUAD)
 
 
-def unpack_strip(strip: np.ndarray, dtype: str = "bf16"):
-    """Inverse of pack_strip -> (engine packing uint8 [N, K/2], scale, mn)."""
-    S, G = strip.shape[:2]
-    words = np.ascontiguousarray(strip).view(np.uint32).reshape(S, G, 272)
-    w = words[..., :256].reshape(S, G, 64, 4)
-    a = np.zeros((S, G, 64, 4, 8), dtype=np.uint32)
+def unpack_quads(quads: np.ndarray, K: int, dtype: str = "bf16"):
+    """Inverse of pack_quads (padding dropped) -> (engine packing uint8 [N, K/2], scale, mn)."""
+    S, nq = quads.shape[:2]
+    Gp, G = nq * 4, K // GROUP
+    words = np.ascontiguousarray(quads).view(np.uint32).reshape(S, nq, QUAD // 4)
+    w = words[..., :1024].reshape(S, Gp, 64, 4)
+    a = np.zeros((S, Gp, 64, 4, 8), dtype=np.uint32)
     for p in range(8):
         a[..., NIBBLE_K[p]] = (w >> np.uint32(4 * p)) & 0xF
-    a = a.reshape(S, G, 4, 16, 4, 8).transpose(0, 3, 1, 2, 4, 5).reshape(S * 16, G * GROUP)
-    sm = words[..., 256:].transpose(0, 2, 1).reshape(S * 16, G)
+    a = a.reshape(S, Gp, 4, 16, 4, 8).transpose(0, 3, 1, 2, 4, 5).reshape(S * 16, Gp * GROUP)[:, :K]
+    sm = words[..., 1024:].reshape(S, nq, 16, 4).transpose(0, 2, 1, 3).reshape(S * 16, Gp)[:, :G]
     scale = from_bits((sm & 0xFFFF).astype(np.uint16), dtype)
     mn = from_bits((sm >> 16).astype(np.uint16), dtype)
     return pack_engine(a.astype(np.uint8)), scale, mn

@@ -54,3 +54,12 @@ def test_shape_errors_are_codes_not_crashes():
     assert lib.tr_int4_gemm(None, None, None, None, None, 0, 8, 128, 5120, 128, 0, 0, None) == _lib.ERR_ARG
     assert lib.tr_pack_int4(None, None, None, None, 16, 128, None) == _lib.ERR_ARG
     assert lib.tr_partial_slots(100, 128, 1) == -1
+
+
+def test_packed_bytes():
+    from tokenrush_amd import _lib
+    lib = _lib.lib()
+    assert lib.tr_packed_bytes(34816, 5120) == 34816 // 16 * 10 * 4352 == 34816 * 5120 // 2 + 4 * 34816 * 5120 // 128
+    assert lib.tr_packed_bytes(16, 384) == 4352                       # 3 groups padded to one quad
+    assert lib.tr_packed_bytes(100, 5120) == 0 and lib.tr_packed_bytes(16, 100) == 0
+    assert lib.tr_packed_bytes(1 << 20, 1 << 15) == 0                 # 2 GiB or more: unsupported

@@ -38,7 +38,7 @@ def check_close(y: torch.Tensor, ref: np.ndarray, what=""):
     assert np.all(err <= np.abs(ref) * 2 ** -8 + amax * 2 ** -14), (what, (err - np.abs(ref) * 2 ** -8).max())
 
 
-@pytest.mark.parametrize("N,K", [(5120, 6144), (256, 5120), (1280, 5120), (5120, 17408)])
+@pytest.mark.parametrize("N,K", [(5120, 6144), (256, 5120), (1280, 5120), (5120, 17408), (256, 384), (512, 2176)])
 def test_pack_matches_oracle(dev, N, K):
     from tokenrush_amd import gfx950
     say(f"pack N={N} K={K}")
@@ -46,13 +46,15 @@ def test_pack_matches_oracle(dev, N, K):
     q, sd, md = dev_weights(p, s, m, "bf16")
     B, sp, mp = gfx950.pack(q, sd, md)
     torch.cuda.synchronize()
-    assert B.shape == (N // 16, K // 128, 1088)
-    assert np.array_equal(B.cpu().numpy(), o.pack_strip(p, s, m, "bf16"))
-    q2, s2, m2 = gfx950.unpack(B, sp, mp)
+    assert B.shape == (N // 16, o.padded_groups(K) // 4, 4352)
+    assert np.array_equal(B.cpu().numpy(), o.pack_quads(p, s, m, "bf16"))
+    assert torch.equal(sp[:, :, :, :].reshape(N // 16, -1, 16, 4).permute(0, 2, 1, 3).reshape(N, -1)[:, :K // 128], sd)
+    q2, s2, m2 = gfx950.unpack(B, sp, mp, K)
     assert torch.equal(q, q2) and torch.equal(sd, s2) and torch.equal(md, m2)
 
 
-@pytest.mark.parametrize("N,K", [(5120, 6144), (256, 5120), (1280, 5120), (14336, 5120), (5120, 17408)])
+@pytest.mark.parametrize("N,K", [(5120, 6144), (256, 5120), (1280, 5120), (14336, 5120), (5120, 17408),
+                                 (256, 384), (1280, 2176), (512, 128)])
 @pytest.mark.parametrize("M", [1, 3, 8, 16])
 def test_mul_matches_oracle(dev, N, K, M):
     from tokenrush_amd import gfx950
@@ -207,7 +209,7 @@ def test_qlinear_api(dev):
     qd, sd, md = dev_weights(p, s, m, "bf16")
     lin = QLinear(qd, sd, md, split_k=4)
     assert lin.shape == (512, 1024) and lin.backend == "gfx950" and lin.group == 128
-    assert lin.nbytes == 512 // 16 * 8 * 1088
+    assert lin.nbytes == 512 // 16 * 2 * 4352
     x = o.make_x(8, 1024, seed=17)
     ref = o.gemm_exact(x, p, s, m)
     check_close(lin(dev_x(x)), ref, "call")

@@ -103,25 +103,29 @@ def test_gemm_dequant_is_within_reference_tolerance():
     assert np.abs(o.gemm_dequant(x, p, s, m) - ref).max() <= np.abs(ref).max() * 2 ** -7
 
 
-def test_pack_strip_per_element():
-    """The strip layout, element by element, from its definition: code (n, k) sits in tile
-    (n // 16, k // 128), lane 16 * c + n % 16 with c = (k % 128) // 32, word j = (k % 32) // 8,
-    nibble p with NIBBLE_K[p] == k % 8; row n's (scale, min) bits at byte 1024 + 4 (n % 16)."""
-    p, s, m = o.make_weights(32, 256, seed=10, dtype="fp16")
+def test_pack_quads_per_element():
+    """The quad layout, element by element, from its definition: code (n, k) sits in quad
+    (n // 16, g // 4) with g = k // 128, block t = g % 4 at byte 1024 t, lane 16 c + n % 16 with
+    c = (k % 128) // 32, word j = (k % 32) // 8, nibble p with NIBBLE_K[p] == k % 8; row n's
+    (scale, min) bits of group g at byte 4096 + 16 (n % 16) + 4 t. K = 640 has 5 groups, so the
+    second quad holds 3 zero padding groups."""
+    p, s, m = o.make_weights(32, 640, seed=10, dtype="fp16")
     codes = o.unpack_int4(p)
-    st = o.pack_strip(p, s, m, "fp16")
-    assert st.shape == (2, 2, 1088)
-    words = st.view(np.uint32).reshape(2, 2, 272)
+    st = o.pack_quads(p, s, m, "fp16")
+    assert st.shape == (2, 2, 4352)
+    words = st.view(np.uint32).reshape(2, 2, 1088)
     inv = {int(k): pp for pp, k in enumerate(o.NIBBLE_K)}
     for n in range(32):
-        for k in range(256):
-            c, j = (k % 128) // 32, (k % 32) // 8
-            w = int(words[n // 16, k // 128, 4 * (16 * c + n % 16) + j])
+        for k in range(640):
+            g, c, j = k // 128, (k % 128) // 32, (k % 32) // 8
+            w = int(words[n // 16, g // 4, 256 * (g % 4) + 4 * (16 * c + n % 16) + j])
             assert (w >> (4 * inv[k % 8])) & 0xF == codes[n, k]
-        for g in range(2):
-            sm = int(words[n // 16, g, 256 + n % 16])
+        for g in range(5):
+            sm = int(words[n // 16, g // 4, 1024 + 4 * (n % 16) + g % 4])
             assert sm & 0xFFFF == int(o.to_bits(s[n, g], "fp16")) and sm >> 16 == int(o.to_bits(m[n, g], "fp16"))
-    p2, s2, m2 = o.unpack_strip(st, "fp16")
+    assert not words[:, 1, 256:1024].any()                                      # padding codes
+    assert not words[:, 1, 1024:].reshape(2, 16, 4)[:, :, 1:].any()             # padding scale/min
+    p2, s2, m2 = o.unpack_quads(st, 640, "fp16")
     assert np.array_equal(p2, p) and np.array_equal(s2, s) and np.array_equal(m2, m)
 
 

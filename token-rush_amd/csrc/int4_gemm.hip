@@ -18,15 +18,20 @@
 // of an M = 1 call is bit-identical to row i of an M = 16 call (the property the reference's
 // tests/test_marlin.py:42-52 checks for Marlin), and likewise within M = 17..32.
 //
-// Weight layout ("strip layout", made once at load time by tr_pack_int4): one 1088-byte tile
-// per (16-row strip, group of 128), tiles of a strip contiguous along K:
-//   packed[N/16][K/128][1088]
-//   bytes [0, 1024): lane l's 16 bytes at 16 l hold row l%16, k in [32 (l/16), 32 (l/16) + 32)
-//     of the group as four 32-bit words; word j covers k0 = 32 (l/16) + 8 j .. k0 + 7 with code
-//     k0 + 2p in nibble p and k0 + 2p + 1 in nibble p + 4 (p = 0..3), so
-//     (w >> 4p) & 0x000F000F is the bf16 pair (k0 + 2p, k0 + 2p + 1) once the exponent is set.
-//   bytes [1024, 1088): row i's scale (low 16 bits) and min (high 16 bits) at 1024 + 4 i.
-// A wave reads a tile with one 16-byte load per lane (1 KiB, contiguous) plus one 4-byte load.
+// Weight layout ("quad layout", made once at load time by tr_pack_int4): the K/128 groups of a
+// 16-row strip are padded to a multiple of four (padding groups have zero codes, scale and min,
+// so they contribute exactly 0) and stored as quads of four groups, 4352 bytes each
+// (34 cache lines of 128 B, so no line is shared by two loads):
+//   packed[N/16][Gp/4][4352]
+//   bytes [1024 t, 1024 t + 1024): the codes of group 4 q + t. Lane l's 16 bytes at 16 l hold
+//     row l % 16, k in [32 (l/16), 32 (l/16) + 32) of the group as four 32-bit words; word j
+//     covers k0 = 32 (l/16) + 8 j .. k0 + 7 with code k0 + 2p in nibble p and k0 + 2p + 1 in
+//     nibble p + 4 (p = 0..3), so (w >> 4p) & 0x000F000F is the bf16 pair (k0 + 2p, k0 + 2p + 1)
+//     once the exponent is set.
+//   bytes [4096, 4352): row i's scale (low 16 bits) and min (high 16 bits) of group 4 q + t at
+//     4096 + 16 i + 4 t, so one 16-byte load gives a lane its row's parameters for all four groups.
+// A wave reads one strip's four groups with four 16-byte loads per lane plus one 16-byte load
+// of parameters, all at one scalar offset.
 //
 // Work split ("activation-stationary"): a workgroup owns a range of strips and a K slot; each
 // of its W waves owns one K block of GW groups (GW = 4 for M <= 16, 2 above), loads that
@@ -40,35 +45,62 @@
 namespace tr {
 
 constexpr int kGroup = 128;
-constexpr int kTileBytes = 1088;
+constexpr int kQuad = 4;                          // groups per quad
+constexpr int kCodeBytes = 1024;                  // one group's codes for 16 rows
+constexpr int kSmOff = kQuad * kCodeBytes;        // parameters of the quad's groups
+constexpr int kQuadBytes = kSmOff + 16 * kQuad * 4;  // 4352 = 34 x 128 B
 constexpr int kWsCounterStride = 32;  // ints between workspace counters: one per 128-byte line
                                       // (agent-scope atomics on one line serialize)
 constexpr int kMaxWaves = 12;   // 768 threads: leaves ~170 VGPRs per lane (3 waves per SIMD)
 
+// Groups of a K-long row after padding to whole quads.
+__host__ __device__ __forceinline__ int padded_groups(int K) { return (K / kGroup + kQuad - 1) / kQuad * kQuad; }
+
 enum { OUT_BF16 = 0, OUT_PARTIAL = 1, OUT_BF16_VIA_WS = 2 };
 
-struct Tile {
-  uint4 w;       // this lane's 16 code bytes
-  uint32_t sm;   // scale | min << 16 of row lane % 16
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// One wave's GW groups of one strip: this lane's 16 code bytes per group and its row's
+// scale | min << 16 per group.
+template <int GW>
+struct Strip {
+  uint4 w[GW];
+  uint32_t sm[GW];
 };
 
-// Tile loads go through a buffer resource: the tile's byte offset is wave-uniform (an SGPR)
-// and the lane offsets are loop-invariant VGPRs, so no vector instruction computes addresses.
-// nt (non-temporal): the weights are streamed once. Reads past the resource size return 0.
-__device__ __forceinline__ void load_tile(Tile& t, __amdgpu_buffer_rsrc_t rsrc, int tile_off, int lane_off,
-                                          int sm_off) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off, tile_off, 2 /* nt */);
-  t.w = make_uint4(v.x, v.y, v.z, v.w);
-  t.sm = __builtin_amdgcn_raw_buffer_load_b32(rsrc, sm_off, tile_off, 2 /* nt */);
+// Loads go through a buffer resource: the strip's byte offset is wave-uniform (an SGPR), the
+// lane offsets are loop-invariant VGPRs and the per-group steps are immediates, so no vector
+// instruction computes addresses. nt (non-temporal): the weights are streamed once. The
+// parameters are loaded first: every group's fold needs them, so vmcnt then lets the first
+// group start as soon as its own codes arrive.
+template <int GW>
+__device__ __forceinline__ void load_strip(Strip<GW>& t, __amdgpu_buffer_rsrc_t rsrc, int soff, int lane_off,
+                                           int sm_voff) {
+  if (GW == 4) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, sm_voff, soff, 2 /* nt */);
+    t.sm[0] = v.x;
+    t.sm[1] = v.y;
+    t.sm[2 % GW] = v.z;
+    t.sm[3 % GW] = v.w;
+  } else {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rsrc, sm_voff, soff, 2 /* nt */);
+    t.sm[0] = v.x;
+    t.sm[1] = v.y;
+  }
+#pragma unroll
+  for (int gw = 0; gw < GW; ++gw) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off + gw * kCodeBytes, soff, 2 /* nt */);
+    t.w[gw] = make_uint4(v.x, v.y, v.z, v.w);
+  }
 }
 
 // E = sum over the group of x * (128 + q), then acc += s * E + (mn - 128 s) * X.
 template <int MT, bool F16S>
-__device__ __forceinline__ void tile_mac(const Tile& t, const uint4 (&xa)[MT][4], const f32x4 (&X)[MT],
+__device__ __forceinline__ void tile_mac(const uint4& w, uint32_t sm, const uint4 (&xa)[MT][4], const f32x4 (&X)[MT],
                                          f32x4 (&acc)[MT], uint32_t kExp128) {
   const uint32_t kMask = 0x000F000Fu;
-  const uint32_t wd[4] = {t.w.x, t.w.y, t.w.z, t.w.w};
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
   bf16x8 b[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -81,11 +113,11 @@ __device__ __forceinline__ void tile_mac(const Tile& t, const uint4 (&xa)[MT][4]
   }
   float sf, mf;
   if (F16S) {
-    sf = f16_bits_to_f32(t.sm & 0xFFFFu);
-    mf = f16_bits_to_f32(t.sm >> 16);
+    sf = f16_bits_to_f32(sm & 0xFFFFu);
+    mf = f16_bits_to_f32(sm >> 16);
   } else {
-    sf = __uint_as_float(t.sm << 16);
-    mf = __uint_as_float(t.sm & 0xFFFF0000u);
+    sf = __uint_as_float(sm << 16);
+    mf = __uint_as_float(sm & 0xFFFF0000u);
   }
   const float c1 = fmaf(-128.f, sf, mf);  // mn - 128 s: removes the +128 code offset
 #pragma unroll
@@ -117,8 +149,9 @@ struct GemmArgs {
 // column n = 16 strip + lane % 16.
 template <int MT, int GW, bool F16S>
 __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
-  extern __shared__ float red[];  // [2][W][MT][64][4]
+  extern __shared__ float red[];  // [2][RB][W][MT][64][4]
   const int G = a.K / kGroup;
+  const int Gp = padded_groups(a.K);
   const int nstrips = a.N / 16;
   const int W = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -128,28 +161,28 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   const int r0 = rbi * a.R;
   const int r1 = min(nstrips, r0 + a.R);
 
-  const int nb = (G + GW - 1) / GW;                    // K blocks
+  const int nb = Gp / GW;                              // K blocks (GW divides a quad)
   const int b0 = (int)(((long)slot * nb) / a.S), b1 = (int)(((long)(slot + 1) * nb) / a.S);
   const int nw = b1 - b0;                              // active waves of this slot
   const bool active = wave < nw;
-  const int blk = b0 + min(wave, nw - 1);
-  const int gbase = blk * GW;
-  const int ng = min(GW, G - gbase);                   // groups in this block (1..GW)
+  const int gbase = (b0 + min(wave, nw - 1)) * GW;     // first group of this wave's block
 
   const uint32_t kExp128 = vgpr_const(0x43004300u);
 
-  // Tile pointer of (strip r, group gbase + gw); clamped so that loads past the end re-read a
-  // valid tile (keeps every loop path's load count equal; those values are never used).
-  auto tile_off = [&](int r, int gw) {
-    const int rr = min(r, r1 - 1);
-    const int g = gbase + min(gw, ng - 1);
-    return __builtin_amdgcn_readfirstlane((rr * G + g) * kTileBytes);
-  };
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a.packed, (short)0, (int)((size_t)nstrips * G * kTileBytes), 0x00020000);
-  const int lane_off = 16 * lane, sm_off = 1024 + 4 * (lane & 15);
+  // Byte offset of this wave's groups in strip r. Strips past the range get an offset beyond
+  // the buffer resource's size: the hardware returns zeros for those loads without touching
+  // memory, so every loop path issues the same loads (no vmcnt drain) and none re-reads HBM.
+  const int quad_stride = Gp / kQuad * kQuadBytes;
+  const int blk_off = gbase / kQuad * kQuadBytes + gbase % kQuad * kCodeBytes;
+  const int oob = nstrips * quad_stride;
+  auto strip_off = [&](int r) { return __builtin_amdgcn_readfirstlane(r < r1 ? r * quad_stride + blk_off : oob); };
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.packed, (short)0, oob, 0x00020000);
+  const int lane_off = 16 * lane;
+  // parameters of row lane % 16, groups gbase % 4 .. + GW - 1, relative to the strip offset
+  const int sm_voff = kSmOff + 16 * (lane & 15) + 4 * (gbase % kQuad) - (gbase % kQuad) * kCodeBytes;
 
-  // Activations of this wave's K block, in registers for the whole strip loop.
+  // Activations of this wave's K block, in registers for the whole strip loop. Padding groups
+  // (g >= G) read group G - 1: finite values that meet zero scale and min.
   uint4 xa[GW][MT][4];
   f32x4 X[GW][MT];
   {
@@ -165,15 +198,13 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
       }
     }
   }
-  // Two strips of tiles in flight, refilled tile by tile. Issued after the activation loads:
-  // vmcnt counts loads in issue order, so the ones-MFMA below waits only for the (L2-resident)
-  // activations and each tile_mac only for its own tile.
-  Tile buf[2][GW];
+  // Two strips in flight. Issued after the activation loads: vmcnt counts loads in issue
+  // order, so the ones-MFMA below waits only for the (L2-resident) activations and each
+  // tile_mac only for its own strip's loads.
+  Strip<GW> buf[2];
   if (active) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int gw = 0; gw < GW; ++gw) load_tile(buf[h][gw], rsrc, tile_off(r0 + h, gw), lane_off, sm_off);
+    load_strip<GW>(buf[0], rsrc, strip_off(r0), lane_off, sm_voff);
+    load_strip<GW>(buf[1], rsrc, strip_off(r0 + 1), lane_off, sm_voff);
   }
 
   {
@@ -195,6 +226,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // barrier per batch); batches alternate between two halves of the LDS ring, so the next
   // batch's writes never race the previous batch's reads.
   const int RB = a.RB;
+  int sib = 0, half = 0;  // position in the current batch, ring half (wave-uniform)
   for (int rb = r0; rb < r1; rb += 2) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -205,12 +237,9 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
         for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (active) {
 #pragma unroll
-          for (int gw = 0; gw < GW; ++gw) {
-            if (gw < ng) tile_mac<MT, F16S>(buf[h][gw], xa[gw], X[gw], acc, kExp128);
-            load_tile(buf[h][gw], rsrc, tile_off(r + 2, gw), lane_off, sm_off);
-          }
+          for (int gw = 0; gw < GW; ++gw) tile_mac<MT, F16S>(buf[h].w[gw], buf[h].sm[gw], xa[gw], X[gw], acc, kExp128);
+          load_strip<GW>(buf[h], rsrc, strip_off(r + 2), lane_off, sm_voff);
         }
-        const int sib = (r - r0) % RB, half = ((r - r0) / RB) & 1;
         float* ring = red + (size_t)half * RB * W * MT * 256;
         if (active) {
 #pragma unroll
@@ -241,6 +270,10 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
               __hip_atomic_store(a.ws_part + ((size_t)slot * a.M + m) * a.N + n, v, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
           }
+          sib = 0;
+          half ^= 1;
+        } else {
+          ++sib;
         }
       }
     }
@@ -274,22 +307,29 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 // ----------------------------------------------------------------------------- layout kernels
 
 // Engine packing (uint8 [N, K/2], element 2j in the low nibble of byte j; tokenrush/quant.py:9-10)
-// plus scale/min [N, K/128] -> strip layout. One thread per output 32-bit word (272 per tile).
+// plus scale/min [N, K/128] -> quad layout. One thread per output 32-bit word (1088 per quad);
+// padding groups are written as zeros.
 __global__ void pack_kernel(const uint32_t* __restrict__ q, const uint16_t* __restrict__ scale,
                             const uint16_t* __restrict__ mn, uint32_t* __restrict__ packed, int N, int K) {
-  const int G = K / kGroup;
-  const size_t total = (size_t)N / 16 * G * (kTileBytes / 4);
+  const int G = K / kGroup, nq = padded_groups(K) / kQuad;
+  constexpr int kWords = kQuadBytes / 4;
+  const size_t total = (size_t)N / 16 * nq * kWords;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int d = i % (kTileBytes / 4);
-    const size_t tile = i / (kTileBytes / 4);
-    const int g = tile % G;
-    const size_t strip = tile / G;
-    if (d >= 256) {
-      const size_t n = strip * 16 + (d - 256);
-      packed[i] = (uint32_t)scale[n * G + g] | ((uint32_t)mn[n * G + g] << 16);
+    const int d = i % kWords;
+    const size_t quad = i / kWords;
+    const size_t strip = quad / nq;
+    const int q0 = (int)(quad % nq) * kQuad;
+    if (d >= kSmOff / 4) {
+      const int e = d - kSmOff / 4, g = q0 + (e & 3);
+      const size_t n = strip * 16 + (e >> 2);
+      packed[i] = g < G ? (uint32_t)scale[n * G + g] | ((uint32_t)mn[n * G + g] << 16) : 0u;
       continue;
     }
-    const int j = d & 3, lane = d >> 2;
+    const int g = q0 + d / 256, j = d & 3, lane = (d & 255) >> 2;
+    if (g >= G) {
+      packed[i] = 0u;
+      continue;
+    }
     const size_t n = strip * 16 + (lane & 15);
     const int k0 = g * kGroup + 32 * (lane >> 4) + 8 * j;
     const uint32_t u = q[(n * K + k0) / 8];  // bytes b0..b3 = codes k0..k0+7
@@ -304,24 +344,28 @@ __global__ void pack_kernel(const uint32_t* __restrict__ q, const uint16_t* __re
   }
 }
 
-// Strip layout -> engine packing and scale/min (the inverse of pack_kernel).
+// Quad layout -> engine packing and scale/min (the inverse of pack_kernel; padding is dropped).
 __global__ void unpack_kernel(const uint32_t* __restrict__ packed, uint32_t* __restrict__ q,
                               uint16_t* __restrict__ scale, uint16_t* __restrict__ mn, int N, int K) {
-  const int G = K / kGroup;
-  const size_t total = (size_t)N / 16 * G * (kTileBytes / 4);
+  const int G = K / kGroup, nq = padded_groups(K) / kQuad;
+  constexpr int kWords = kQuadBytes / 4;
+  const size_t total = (size_t)N / 16 * nq * kWords;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int d = i % (kTileBytes / 4);
-    const size_t tile = i / (kTileBytes / 4);
-    const int g = tile % G;
-    const size_t strip = tile / G;
+    const int d = i % kWords;
+    const size_t quad = i / kWords;
+    const size_t strip = quad / nq;
+    const int q0 = (int)(quad % nq) * kQuad;
     const uint32_t w = packed[i];
-    if (d >= 256) {
-      const size_t n = strip * 16 + (d - 256);
+    if (d >= kSmOff / 4) {
+      const int e = d - kSmOff / 4, g = q0 + (e & 3);
+      if (g >= G) continue;
+      const size_t n = strip * 16 + (e >> 2);
       scale[n * G + g] = (uint16_t)(w & 0xFFFF);
       mn[n * G + g] = (uint16_t)(w >> 16);
       continue;
     }
-    const int j = d & 3, lane = d >> 2;
+    const int g = q0 + d / 256, j = d & 3, lane = (d & 255) >> 2;
+    if (g >= G) continue;
     const size_t n = strip * 16 + (lane & 15);
     const int k0 = g * kGroup + 32 * (lane >> 4) + 8 * j;
     uint32_t u = 0;
@@ -376,6 +420,15 @@ using namespace tr;
 namespace {
 
 constexpr int kCUs = 256;          // MI355X compute units
+
+// Bytes of the quad layout of an N x K weight.
+size_t packed_bytes(int N, int K) { return (size_t)N / 16 * (padded_groups(K) / kQuad) * kQuadBytes; }
+
+// Shapes the kernels take: whole 16-row strips and 128-wide groups, and a packed weight that
+// 32-bit buffer offsets address.
+bool shape_ok(int N, int K) {
+  return N > 0 && K > 0 && N % 16 == 0 && K % kGroup == 0 && packed_bytes(N, K) < ((size_t)1 << 31);
+}
 constexpr int kWavesPerCU = 12;    // occupancy of the GEMM kernel (about 150 VGPRs per lane)
 constexpr size_t kLdsBudget = 64 * 1024;  // dynamic LDS of one workgroup (the default limit)
 
@@ -388,9 +441,9 @@ int group_block(int M) { return M > 16 ? 2 : 4; }
 // Tiling of an N x K weight for M rows. Depends on M only through the row-tile count
 // (M <= 16 or not), so rows are bit-identical for every M within each range.
 bool make_plan(int N, int K, int M, int S_req, int R_req, Plan* p) {
-  const int G = K / kGroup, nstrips = N / 16;
+  const int nstrips = N / 16;
   p->GW = group_block(M);
-  const int nb = (G + p->GW - 1) / p->GW;
+  const int nb = padded_groups(K) / p->GW;
   int S = S_req > 0 ? S_req : (nb + kMaxWaves - 1) / kMaxWaves;
   if (S < 1) S = 1;
   if (S > nb) return false;
@@ -433,7 +486,7 @@ hipError_t launch(const GemmArgs& a, const Plan& p, int scale_dtype, hipStream_t
 extern "C" {
 
 int tr_gemm_plan(int N, int K, int M, int* S, int* W, int* R) {
-  if (N <= 0 || K <= 0 || N % 16 || K % kGroup || M < 1 || M > 32 || !S || !W || !R) return TR_ERR_SHAPE;
+  if (!shape_ok(N, K) || M < 1 || M > 32 || !S || !W || !R) return TR_ERR_SHAPE;
   Plan p;
   if (!make_plan(N, K, M, 0, 0, &p)) return TR_ERR_CONFIG;
   *S = p.S;
@@ -441,6 +494,8 @@ int tr_gemm_plan(int N, int K, int M, int* S, int* W, int* R) {
   *R = p.R;
   return TR_OK;
 }
+
+size_t tr_packed_bytes(int N, int K) { return shape_ok(N, K) ? packed_bytes(N, K) : 0; }
 
 int tr_partial_slots(int N, int K, int M) {
   int S, W, R;
@@ -456,7 +511,7 @@ static size_t ws_counter_bytes() { return (size_t)kWsCounters * kWsCounterStride
 
 size_t tr_gemm_workspace_bytes(int N, int K, int M) {
   Plan p;
-  if (N <= 0 || K <= 0 || N % 16 || K % kGroup || M < 1 || M > 32 || !make_plan(N, K, M, 0, 0, &p)) return 0;
+  if (!shape_ok(N, K) || M < 1 || M > 32 || !make_plan(N, K, M, 0, 0, &p)) return 0;
   if (p.S == 1) return 0;
   return ws_counter_bytes() + (size_t)p.S * M * N * sizeof(float);
 }
@@ -465,7 +520,7 @@ int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials
                     size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots, int R,
                     void* stream) {
   if (group != kGroup) return TR_ERR_CONFIG;
-  if (M < 0 || M > 32 || N <= 0 || K <= 0 || N % 16 || K % kGroup) return TR_ERR_SHAPE;
+  if (M < 0 || M > 32 || !shape_ok(N, K)) return TR_ERR_SHAPE;
   if (M == 0) return TR_OK;
   if (!x || !packed || (!out == !partials)) return TR_ERR_ARG;
   if (scale_dtype != 0 && scale_dtype != 1) return TR_ERR_ARG;
@@ -516,8 +571,8 @@ static int grid_for(size_t work) {
 
 int tr_pack_int4(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K, void* stream) {
   if (!qweight || !scale || !mn || !packed) return TR_ERR_ARG;
-  if (N <= 0 || K <= 0 || N % 16 || K % kGroup) return TR_ERR_SHAPE;
-  const size_t total = (size_t)N / 16 * (K / kGroup) * (kTileBytes / 4);
+  if (!shape_ok(N, K)) return TR_ERR_SHAPE;
+  const size_t total = packed_bytes(N, K) / 4;
   hipLaunchKernelGGL(pack_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, (const uint32_t*)qweight,
                      (const uint16_t*)scale, (const uint16_t*)mn, (uint32_t*)packed, N, K);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
@@ -525,8 +580,8 @@ int tr_pack_int4(const void* qweight, const void* scale, const void* mn, void* p
 
 int tr_unpack_int4(const void* packed, void* qweight, void* scale, void* mn, int N, int K, void* stream) {
   if (!qweight || !packed || !scale || !mn) return TR_ERR_ARG;
-  if (N <= 0 || K <= 0 || N % 16 || K % kGroup) return TR_ERR_SHAPE;
-  const size_t total = (size_t)N / 16 * (K / kGroup) * (kTileBytes / 4);
+  if (!shape_ok(N, K)) return TR_ERR_SHAPE;
+  const size_t total = packed_bytes(N, K) / 4;
   hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream,
                      (const uint32_t*)packed, (uint32_t*)qweight, (uint16_t*)scale, (uint16_t*)mn, N, K);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;

@@ -26,6 +26,7 @@ SIGNATURES = {
     "tr_gemm_plan": (_I, [_I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "tr_partial_slots": (_I, [_I, _I, _I]),
     "tr_gemm_workspace_bytes": (_S, [_I, _I, _I]),
+    "tr_packed_bytes": (_S, [_I, _I]),
     "tr_int4_gemm": (_I, [_P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _I, _P]),
     "tr_int4_gemm_ex": (_I, [_P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _I, _I, _P]),
     "tr_pack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),

@@ -5,9 +5,11 @@ converts the engine's packing to the kernel's weight layout and back, sizes the 
 before graph capture, and launches the kernel. The kernel (csrc/int4_gemm.hip) is our own
 design, not Marlin:
 
-* weight layout: uint8 [N/16, K/128, 1088] -- one tile per (16-row strip, group of 128):
-  1 KiB of codes in the order one wave's 16-byte loads consume them, then the 16 rows'
-  (scale, min) pairs, so a strip is one contiguous stream;
+* weight layout ("quad layout"): uint8 [N/16, Gp/4, 4352], Gp = K/128 rounded up to a multiple
+  of 4 (padding groups are zeros). One quad per (16-row strip, four groups of 128): 4 x 1 KiB of
+  codes in the order one wave's 16-byte loads consume them, then the 16 rows' (scale, min)
+  pairs for the four groups (16 bytes per row). A strip is one contiguous stream of whole
+  128-byte lines;
 * every M in 1..16 runs the same instructions (rows beyond M are padding lanes), so each
   output row is bit-identical for every M, as Marlin's is (reference test_marlin.py:42-52);
   the same holds within M = 17..32;
@@ -25,7 +27,8 @@ import torch
 from . import _lib
 
 GROUP = 128
-TILE = 1088
+QUAD = 4352          # bytes of one (16-row strip, 4 groups) quad
+SM_OFF = 4096        # offset of the quad's scale/min words
 MAX_ROWS = 32        # two 16-row MFMA tiles
 SCALE_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 WS_COUNTER_BYTES = 4096 * 128   # the workspace's counter region (one counter per 128-byte line)
@@ -46,20 +49,26 @@ def available() -> bool:
         return False
 
 
+def padded_groups(K: int) -> int:
+    """K/128 rounded up to whole quads of four groups."""
+    return -(-(K // GROUP) // 4) * 4
+
+
 def _check_shape(N: int, K: int):
-    if N % 16 or K % GROUP or N <= 0 or K <= 0:
-        raise RuntimeError(f"problem shape (n={N}, k={K}) not supported: need n % 16 == 0, k % {GROUP} == 0")
+    if N % 16 or K % GROUP or N <= 0 or K <= 0 or int(ext().tr_packed_bytes(N, K)) == 0:
+        raise RuntimeError(f"problem shape (n={N}, k={K}) not supported: need n % 16 == 0, k % {GROUP} == 0 "
+                           f"and a packed size below 2 GiB")
 
 
 def _sm_views(B: torch.Tensor, dtype):
-    """(scale, min) as strided views [N/16, K/128, 16] into the tiles of B."""
-    sm = B[..., 1024:].view(dtype).unflatten(-1, (16, 2))
+    """(scale, min) as strided views [N/16, Gp/4, 16 rows, 4 groups] into the quads of B."""
+    sm = B[..., SM_OFF:].view(dtype).unflatten(-1, (16, 4, 2))
     return sm[..., 0], sm[..., 1]
 
 
 def pack(qweight: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor):
-    """Engine packing (uint8 [N, K/2], bf16/fp16 [N, K/128] x2) -> (B, s, m): B is the strip
-    layout uint8 [N/16, K/128, 1088] holding codes, scale and min; s and m are views into B
+    """Engine packing (uint8 [N, K/2], bf16/fp16 [N, K/128] x2) -> (B, s, m): B is the quad
+    layout uint8 [N/16, Gp/4, 4352] holding codes, scale and min; s and m are views into B
     (they carry the scale dtype). The counterpart of marlin.pack (marlin.py:73-96)."""
     _lib.require_gpu(qweight, scale, mn)
     N, K = qweight.shape[0], qweight.shape[1] * 2
@@ -69,17 +78,21 @@ def pack(qweight: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor):
     if scale.dtype not in SCALE_DTYPES or mn.dtype != scale.dtype:
         raise RuntimeError("scale/min must both be bf16 or fp16")
     q, s, m = qweight.contiguous(), scale.contiguous(), mn.contiguous()
-    B = torch.empty(N // 16, K // GROUP, TILE, dtype=torch.uint8, device=q.device)
+    B = torch.empty(N // 16, padded_groups(K) // 4, QUAD, dtype=torch.uint8, device=q.device)
     _lib.check(ext().tr_pack_int4(_lib.ptr(q), _lib.ptr(s), _lib.ptr(m), _lib.ptr(B), N, K, _lib.stream_of(q)),
                "tr_pack_int4")
     return (B,) + _sm_views(B, scale.dtype)
 
 
-def unpack(B: torch.Tensor, s: torch.Tensor, m: torch.Tensor):
+def unpack(B: torch.Tensor, s: torch.Tensor, m: torch.Tensor, K: int = None):
     """Inverse of pack -> (qweight uint8 [N, K/2], scale [N, K/128], mn [N, K/128])
-    (marlin.unpack, marlin.py:99-118). s only supplies the scale dtype."""
+    (marlin.unpack, marlin.py:99-118). s only supplies the scale dtype. K defaults to the
+    padded width; pass the true K when K/128 is not a multiple of 4."""
     _lib.require_gpu(B)
-    N, K = B.shape[0] * 16, B.shape[1] * GROUP
+    N = B.shape[0] * 16
+    K = B.shape[1] * 4 * GROUP if K is None else K
+    if padded_groups(K) != B.shape[1] * 4:
+        raise RuntimeError(f"K = {K} does not match the packed weight ({B.shape[1]} quads per strip)")
     q = torch.empty(N, K // 2, dtype=torch.uint8, device=B.device)
     sc = torch.empty(N, K // GROUP, dtype=s.dtype, device=B.device)
     mn = torch.empty_like(sc)
@@ -126,7 +139,7 @@ def _launch(x, B, s, y, partial, n_slots, strips_per_wg=-1, slots=0):
         raise RuntimeError("dtypes: x must be bf16, scale/min bf16 or fp16")
     if not (x.is_contiguous() and B.is_contiguous()):
         raise RuntimeError("inputs must be contiguous")
-    if M > MAX_ROWS or K != B.shape[1] * GROUP or B.shape[2] != TILE:
+    if M > MAX_ROWS or K % GROUP or padded_groups(K) != B.shape[1] * 4 or B.shape[2] != QUAD:
         raise RuntimeError(f"problem shape (m={M}, n={N}, k={K}) not supported: need m <= {MAX_ROWS}")
     _lib.require_gpu(x, B, y)
     ws, nbytes = None, 0

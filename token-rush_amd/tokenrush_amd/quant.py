@@ -93,7 +93,7 @@ class QLinear:
     def nibbles(self):
         """(qweight, scale, mn) in the engine's packing (unpacked from the strip layout if needed)."""
         if self.backend == "gfx950":
-            return gfx950.unpack(self.B, self.s, self.m)
+            return gfx950.unpack(self.B, self.s, self.m, self.shape_[1])
         return self.qweight, self.scale, self.mn
 
     def rows(self, ids: torch.Tensor):
