@@ -95,10 +95,21 @@ __device__ __forceinline__ void load_strip(Strip<GW>& t, __amdgpu_buffer_rsrc_t 
   }
 }
 
-// E = sum over the group of x * (128 + q), then acc += s * E + (mn - 128 s) * X.
+// Scale of a (scale | min << 16) word, fp32.
+template <bool F16S>
+__device__ __forceinline__ float sm_scale(uint32_t sm) {
+  return F16S ? f16_bits_to_f32(sm & 0xFFFFu) : __uint_as_float(sm << 16);
+}
+template <bool F16S>
+__device__ __forceinline__ float sm_min(uint32_t sm) {
+  return F16S ? f16_bits_to_f32(sm >> 16) : __uint_as_float(sm & 0xFFFF0000u);
+}
+
+// E = sum over the group of x * (128 + q), then acc += s * E. The group's other term,
+// (mn - 128 s) * sum(x), is added once per strip by min_fold.
 template <int MT, bool F16S>
-__device__ __forceinline__ void tile_mac(const uint4& w, uint32_t sm, const uint4 (&xa)[MT][4], const f32x4 (&X)[MT],
-                                         f32x4 (&acc)[MT], uint32_t kExp128) {
+__device__ __forceinline__ void tile_mac(const uint4& w, uint32_t sm, const uint4 (&xa)[MT][4], f32x4 (&acc)[MT],
+                                         uint32_t kExp128) {
   const uint32_t kMask = 0x000F000Fu;
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
   bf16x8 b[4];
@@ -111,15 +122,7 @@ __device__ __forceinline__ void tile_mac(const uint4& w, uint32_t sm, const uint
     d.w = ((wd[j] >> 12) & kMask) | kExp128;
     b[j] = __builtin_bit_cast(bf16x8, d);
   }
-  float sf, mf;
-  if (F16S) {
-    sf = f16_bits_to_f32(sm & 0xFFFFu);
-    mf = f16_bits_to_f32(sm >> 16);
-  } else {
-    sf = __uint_as_float(sm << 16);
-    mf = __uint_as_float(sm & 0xFFFF0000u);
-  }
-  const float c1 = fmaf(-128.f, sf, mf);  // mn - 128 s: removes the +128 code offset
+  const float sf = sm_scale<F16S>(sm);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     f32x4 E = {0.f, 0.f, 0.f, 0.f};
@@ -127,11 +130,27 @@ __device__ __forceinline__ void tile_mac(const uint4& w, uint32_t sm, const uint
     for (int j = 0; j < 4; ++j)
       E = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[mt][j]), b[j], E, 0, 0, 0);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      acc[mt][r] = fmaf(sf, E[r], acc[mt][r]);
-      acc[mt][r] = fmaf(c1, X[mt][r], acc[mt][r]);
-    }
+    for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(sf, E[r], acc[mt][r]);
   }
+}
+
+// acc[m][n] += sum over the wave's groups t of (mn - 128 s)[n, t] * X[m, t], X = sum of x over
+// group t: one 16 x 16 x 4 fp32 MFMA per row tile with the group slot as k. A (Xa) holds
+// X[m = lane % 16][t = lane / 16]; B is built here: lane l takes its row's parameters of group
+// slot l / 16 (slots >= GW carry zero).
+template <int MT, int GW, bool F16S>
+__device__ __forceinline__ void min_fold(const uint32_t (&sm)[GW], const float (&Xa)[MT], int slot, f32x4 (&acc)[MT]) {
+  uint32_t w;
+  if (GW == 4) {
+    const uint32_t a01 = (slot & 1) ? sm[1] : sm[0];
+    const uint32_t a23 = (slot & 1) ? sm[3 % GW] : sm[2 % GW];
+    w = (slot & 2) ? a23 : a01;
+  } else {
+    w = slot == 0 ? sm[0] : slot == 1 ? sm[1 % GW] : 0u;
+  }
+  const float c1 = fmaf(-128.f, sm_scale<F16S>(w), sm_min<F16S>(w));  // mn - 128 s: removes the code offset
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(Xa[mt], c1, acc[mt], 0, 0, 0);
 }
 
 struct GemmArgs {
@@ -184,7 +203,6 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // Activations of this wave's K block, in registers for the whole strip loop. Padding groups
   // (g >= G) read group G - 1: finite values that meet zero scale and min.
   uint4 xa[GW][MT][4];
-  f32x4 X[GW][MT];
   {
 #pragma unroll
     for (int gw = 0; gw < GW; ++gw) {
@@ -199,7 +217,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     }
   }
   // Two strips in flight. Issued after the activation loads: vmcnt counts loads in issue
-  // order, so the ones-MFMA below waits only for the (L2-resident) activations and each
+  // order, so the selector MFMAs below wait only for the (L2-resident) activations and each
   // tile_mac only for its own strip's loads.
   Strip<GW> buf[2];
   if (active) {
@@ -207,20 +225,27 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     load_strip<GW>(buf[1], rsrc, strip_off(r0 + 1), lane_off, sm_voff);
   }
 
+  // Xa[mt] = sum of x over group gbase + lane / 16 for row 16 mt + lane % 16 (the A operand of
+  // min_fold), from MFMAs with x as B and a block selector as A: rows 4 t .. 4 t + 3 of A are
+  // ones against group slot t, so output row i holds the sum for slot i / 4.
+  float Xa[MT];
   {
-    const uint32_t kOnes = 0x3F803F80u;
-    const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(kOnes, kOnes, kOnes, kOnes));
+    const int sel = (lane & 15) >> 2;
 #pragma unroll
-    for (int gw = 0; gw < GW; ++gw)
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 D = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        X[gw][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int gw = 0; gw < GW; ++gw) {
+        const uint32_t one = sel == gw ? 0x3F803F80u : 0u;
+        const bf16x8 A = __builtin_bit_cast(bf16x8, make_uint4(one, one, one, one));
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          X[gw][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[gw][mt][j]), ones,
-                                                              X[gw][mt], 0, 0, 0);
+          D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, xa[gw][mt][j]), D, 0, 0, 0);
       }
+      Xa[mt] = D[0];
+    }
   }
+  const int slot16 = lane >> 4;
 
   // Partial tiles of RB consecutive strips are collected in LDS and reduced together (one
   // barrier per batch); batches alternate between two halves of the LDS ring, so the next
@@ -237,7 +262,8 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
         for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (active) {
 #pragma unroll
-          for (int gw = 0; gw < GW; ++gw) tile_mac<MT, F16S>(buf[h].w[gw], buf[h].sm[gw], xa[gw], X[gw], acc, kExp128);
+          for (int gw = 0; gw < GW; ++gw) tile_mac<MT, F16S>(buf[h].w[gw], buf[h].sm[gw], xa[gw], acc, kExp128);
+          min_fold<MT, GW, F16S>(buf[h].sm, Xa, slot16, acc);
           load_strip<GW>(buf[h], rsrc, strip_off(r + 2), lane_off, sm_voff);
         }
         float* ring = red + (size_t)half * RB * W * MT * 256;
