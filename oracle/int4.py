@@ -89,15 +89,17 @@ def pack_quads(packed: np.ndarray, scale: np.ndarray, mn: np.ndarray, dtype: str
     """Engine packing + scale/min -> the gfx950 quad layout uint8 [N/16, Gp/4, 4352] (the layout
     token-rush_amd/csrc/int4_gemm.hip documents; it has no counterpart in the reference, whose
     load-time repack is Marlin's, marlin.py:73-96). Groups are padded with zeros to Gp, a
-    multiple of 4. Per (strip, quad): four 1024-byte blocks of codes in lane order, then
+    multiple of 4. Per (strip, quad): four 1024-byte blocks of codes in lane order (lane
+    16 c + n, word j holds k = 32 j + 8 c .. + 7 of row n, code k0 + 2p in nibble p and
+    k0 + 2p + 1 in nibble p + 4), then
     16 rows x 4 groups of (scale bits | min bits << 16)."""
     codes = unpack_int4(packed).astype(np.uint32)
     N, K = codes.shape
     S, G, Gp = N // 16, K // GROUP, padded_groups(K)
     c = np.zeros((N, Gp * GROUP), dtype=np.uint32)
     c[:, :K] = codes
-    a = c.reshape(S, 16, Gp, 4, 4, 8)                    # strip, n, g, c, j, kk
-    a = a.transpose(0, 2, 3, 1, 4, 5).reshape(S, Gp, 64, 4, 8)   # lane = 16 c + n
+    a = c.reshape(S, 16, Gp, 4, 4, 8)                    # strip, n, g, j, c, kk: k = 32 j + 8 c + kk
+    a = a.transpose(0, 2, 4, 1, 3, 5).reshape(S, Gp, 64, 4, 8)   # lane = 16 c + n, word j
     words = np.zeros((S, Gp, 64, 4), dtype=np.uint32)
     for p in range(8):
         words |= a[..., NIBBLE_K[p]] << np.uint32(4 * p)
@@ -117,7 +119,7 @@ def unpack_quads(quads: np.ndarray, K: int, dtype: str = "bf16"):
     a = np.zeros((S, Gp, 64, 4, 8), dtype=np.uint32)
     for p in range(8):
         a[..., NIBBLE_K[p]] = (w >> np.uint32(4 * p)) & 0xF
-    a = a.reshape(S, Gp, 4, 16, 4, 8).transpose(0, 3, 1, 2, 4, 5).reshape(S * 16, Gp * GROUP)[:, :K]
+    a = a.reshape(S, Gp, 4, 16, 4, 8).transpose(0, 3, 1, 4, 2, 5).reshape(S * 16, Gp * GROUP)[:, :K]
     sm = words[..., 1024:].reshape(S, nq, 16, 4).transpose(0, 2, 1, 3).reshape(S * 16, Gp)[:, :G]
     scale = from_bits((sm & 0xFFFF).astype(np.uint16), dtype)
     mn = from_bits((sm >> 16).astype(np.uint16), dtype)

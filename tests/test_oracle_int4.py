@@ -106,7 +106,7 @@ def test_gemm_dequant_is_within_reference_tolerance():
 def test_pack_quads_per_element():
     """The quad layout, element by element, from its definition: code (n, k) sits in quad
     (n // 16, g // 4) with g = k // 128, block t = g % 4 at byte 1024 t, lane 16 c + n % 16 with
-    c = (k % 128) // 32, word j = (k % 32) // 8, nibble p with NIBBLE_K[p] == k % 8; row n's
+    c = (k % 32) // 8, word j = (k % 128) // 32, nibble p with NIBBLE_K[p] == k % 8; row n's
     (scale, min) bits of group g at byte 4096 + 16 (n % 16) + 4 t. K = 640 has 5 groups, so the
     second quad holds 3 zero padding groups."""
     p, s, m = o.make_weights(32, 640, seed=10, dtype="fp16")
@@ -117,7 +117,7 @@ def test_pack_quads_per_element():
     inv = {int(k): pp for pp, k in enumerate(o.NIBBLE_K)}
     for n in range(32):
         for k in range(640):
-            g, c, j = k // 128, (k % 128) // 32, (k % 32) // 8
+            g, c, j = k // 128, (k % 32) // 8, (k % 128) // 32
             w = int(words[n // 16, g // 4, 256 * (g % 4) + 4 * (16 * c + n % 16) + j])
             assert (w >> (4 * inv[k % 8])) & 0xF == codes[n, k]
         for g in range(5):

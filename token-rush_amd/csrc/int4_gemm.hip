@@ -24,8 +24,9 @@
 // (34 cache lines of 128 B, so no line is shared by two loads):
 //   packed[N/16][Gp/4][4352]
 //   bytes [1024 t, 1024 t + 1024): the codes of group 4 q + t. Lane l's 16 bytes at 16 l hold
-//     row l % 16, k in [32 (l/16), 32 (l/16) + 32) of the group as four 32-bit words; word j
-//     covers k0 = 32 (l/16) + 8 j .. k0 + 7 with code k0 + 2p in nibble p and k0 + 2p + 1 in
+//     row l % 16 of the group as four 32-bit words; word j covers k0 = 32 j + 8 (l/16) .. k0 + 7
+//     (so MFMA j contracts k in [32 j, 32 j + 32) and the matching activations of one row are 64
+//     contiguous bytes) with code k0 + 2p in nibble p and k0 + 2p + 1 in
 //     nibble p + 4 (p = 0..3), so (w >> 4p) & 0x000F000F is the bf16 pair (k0 + 2p, k0 + 2p + 1)
 //     once the exponent is set.
 //   bytes [4096, 4352): row i's scale (low 16 bits) and min (high 16 bits) of group 4 q + t at
@@ -210,9 +211,9 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int xr = min(16 * mt + (lane & 15), a.M - 1);
-        const uint4* p = (const uint4*)(a.x + (size_t)xr * a.K + g * kGroup + 32 * (lane >> 4));
+        const uint4* p = (const uint4*)(a.x + (size_t)xr * a.K + g * kGroup + 8 * (lane >> 4));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xa[gw][mt][j] = p[j];
+        for (int j = 0; j < 4; ++j) xa[gw][mt][j] = p[4 * j];  // k = 32 j + 8 (lane / 16) .. + 7
       }
     }
   }
@@ -357,7 +358,7 @@ __global__ void pack_kernel(const uint32_t* __restrict__ q, const uint16_t* __re
       continue;
     }
     const size_t n = strip * 16 + (lane & 15);
-    const int k0 = g * kGroup + 32 * (lane >> 4) + 8 * j;
+    const int k0 = g * kGroup + 32 * j + 8 * (lane >> 4);
     const uint32_t u = q[(n * K + k0) / 8];  // bytes b0..b3 = codes k0..k0+7
     uint32_t w = 0;
 #pragma unroll
@@ -393,7 +394,7 @@ __global__ void unpack_kernel(const uint32_t* __restrict__ packed, uint32_t* __r
     const int g = q0 + d / 256, j = d & 3, lane = (d & 255) >> 2;
     if (g >= G) continue;
     const size_t n = strip * 16 + (lane & 15);
-    const int k0 = g * kGroup + 32 * (lane >> 4) + 8 * j;
+    const int k0 = g * kGroup + 32 * j + 8 * (lane >> 4);
     uint32_t u = 0;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
