@@ -17,6 +17,9 @@ roofline    the dominant kernel (gate/up, 53% of the bytes): its algorithmic byt
             kernel alone over all weight copies, on the launch stream; vs 8 TB/s.
 accept      on-device accept latency (BASELINE config 3 and 4): mean per launch over a graph of
             back-to-back calls.
+config5     one verify step of the random-init 64-layer hybrid at M = 8 (257 int4 GEMMs, split-K
+            partial consumers, stand-in mixers, lm_head, greedy accept) captured as one hipGraph;
+            time per replay and weight bytes / time.
 cpu_baseline  the reference's CPU path restated in torch (unpack, in-place dequant, F.linear) on
             one layer set at M = 8, OMP_NUM_THREADS host cores, median of >= 5 passes
             (about 10 s).
@@ -140,6 +143,34 @@ def accept_latency(torch, dev):
     return res
 
 
+def config5_step(torch, dev, M=M_VERIFY, reps=10):
+    """one verify step of the random-init 64-layer hybrid (48 GDN + 16 attention
+    layers, int4 g128 weights, stand-in mixers) + lm_head + greedy accept/commit, captured as one
+    hipGraph (tokenrush_amd.step). Returns the replay time and the weight-streaming rate."""
+    from tokenrush_amd.accept import AcceptState
+    from tokenrush_amd.step import StepConfig, VerifyModel, prepare
+    t0 = time.perf_counter()
+    model = VerifyModel(StepConfig(), device=dev, seed=5)
+    prepare(model, M)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    x0 = torch.randn(M, model.cfg.hidden, device=dev, generator=gen).to(torch.bfloat16)
+    spec = torch.randint(0, model.cfg.vocab, (M,), device=dev, generator=gen)
+    st = AcceptState(M, dev)
+    g = graph_of(torch, lambda: model.step(x0, spec, st))
+    build_s = time.perf_counter() - t0
+    t = timed_graph(torch, g, reps=reps)
+    nbytes = model.nbytes()
+    launches = model.cfg.n_layers * 8 + 3
+    del g, model
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(t * 1e3, 3), "weights_GB": round(nbytes / 1e9, 3),
+            "weight_GBps": round(nbytes / t / 1e9, 1), "launches": launches, "M": M, "replays": reps,
+            "build_s": round(build_s, 1),
+            "note": "one hipGraph: 257 int4 GEMMs, 129 add_rmsnorm (split-K partial consumers), 64 silu_mul, "
+                    "64 stand-in mixers, lm_head 248320x5120, greedy accept/commit"}
+
+
 def cpu_baseline(M=M_VERIFY, min_reps=5, budget_s=10.0):
     """The reference's CPU path restated (oracle.int4.torch_dequant_linear: torch unpack, in-place
     fp16 dequant, F.linear in bf16) over one layer set at M rows on the host's CPU share; median of
@@ -178,6 +209,7 @@ def main():
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer verify-step graph (config 5)")
     ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET],
                     help="profiling aid: run just this projection's launches (M=8) and exit")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -229,6 +261,9 @@ def main():
         xsM = {K: torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16) for _, _, K, _ in LAYER_SET}
         sweep[M] = round(sum(kernel_means(torch, gfx950, copies, xsM, reps=2).values()) * 1e6, 2)
     acc = accept_latency(torch, dev)
+    del copies
+    torch.cuda.empty_cache()
+    c5 = None if a.no_config5 else config5_step(torch, dev)
 
     value = step_bytes[8] * a.steps / wall8 / 1e9
     gu = dict((n, (N, K)) for n, N, K, _ in LAYER_SET)["gate_up"]
@@ -254,6 +289,7 @@ def main():
         "layer_set_us_by_M": {1: round(sum(k1.values()) * 1e6, 2), 8: round(sum(k8.values()) * 1e6, 2), **sweep},
         "accept_us": acc,
         "verify_accept_us_m8": round(sum(k8.values()) * 1e6 + acc["greedy_m8"], 2),
+        "config5_verify_step": c5,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "int4_gemm_kernel gate_up 34816x5120 M=8 (%.2f us)" % (k8["gate_up"] * 1e6)},

@@ -144,6 +144,20 @@ int tr_accept_tree(const void* logits, int M, int V, const int64_t* node_toks, c
 int tr_commit_rows(void* data, int planes, long plane_stride_bytes, int row_bytes, const int64_t* pos,
                    const int64_t* n_accepted, const int64_t* commit, int max_n, void* stream);
 
+/* ---------------------------------------------------------------- row kernels around the GEMMs */
+
+/* Split-K partial consumer: x [T, N] bf16, h per h_mode (0 none, 1 bf16 [T, N], 2 fp32 partials
+ * [n_slots, T, N] summed in slot order then rounded to bf16), weight [N] bf16 ->
+ * xo = bf16(x + h) (not written when h_mode is 0) and y = rmsnorm(xo) * (1 + weight), or
+ * bf16(weight * bf16(rmsnorm(xo))) when plain. N <= 8192; one workgroup per row.
+ * Replaces: add_rmsnorm (tokenrush/fused.py:23-60). */
+int tr_add_rmsnorm(const void* x, const void* h, int h_mode, int n_slots, const void* weight, void* xo, void* y,
+                   int T, int N, float eps, int plain, void* stream);
+
+/* gate_up [T, 2F] bf16 (rows ld >= 2F elements apart; 0 = 2F) -> y [T, F] bf16 = silu(gate) * up.
+ * Replaces: silu_mul (tokenrush/fused.py:67-87). */
+int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

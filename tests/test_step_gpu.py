@@ -1,0 +1,114 @@
+"""The verify-step driver (tokenrush_amd/step.py) on a small hybrid config: the body against a
+torch float reference built from the same weights (dequantized by the bit-exact HIP dequant),
+the greedy accept against the oracle on the step's own logits (bit-exact), and the whole step
+captured as one hipGraph reproducing the eager step bit-for-bit on repeated replays."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as oa
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref_body(model, x0):
+    """Float reference of VerifyModel.body: exact weights q * s + m, fp32 matmuls, the same bf16
+    rounding points as the kernels (projection outputs, residual stream, norm outputs)."""
+    cfg = model.cfg
+    bf = lambda t: t.to(torch.bfloat16).float()
+
+    def lin(L, v):
+        q, s, m = L.nibbles()                       # exact weight q * s + m (what the GEMM folds)
+        codes = torch.stack([q & 0xF, q >> 4], -1).view(q.shape[0], -1).float()
+        G = s.shape[1]
+        W = codes.view(q.shape[0], G, -1) * s.float()[..., None] + m.float()[..., None]
+        return v @ W.view(q.shape[0], -1).t()
+
+    def norm(x, w):
+        return bf(x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.eps) * (1.0 + w.float()))
+
+    def silu_mul(u):
+        F = u.shape[1] // 2
+        g, v = u[:, :F], u[:, F:2 * F]
+        return bf(g / (1 + torch.exp(-g)) * v)
+
+    x = x0.float()
+    h = None
+    for L in model.layers:
+        if h is not None:
+            x = bf(x + bf(h))
+        n = norm(x, L.ln1)
+        u = bf(lin(L.proj, n))
+        y = silu_mul(u[:, :2 * cfg.mixer_out])
+        h = lin(L.out, y)
+        x = bf(x + bf(h))
+        n = norm(x, L.ln2)
+        a = silu_mul(bf(lin(L.gate_up, n)))
+        h = lin(L.down, a)
+    x = bf(x + bf(h))
+    n = norm(x, model.final_norm)
+    return lin(model.lm_head, n)
+
+
+@pytest.fixture(scope="module")
+def small_model(dev):
+    from tokenrush_amd.step import SMALL, VerifyModel
+    return VerifyModel(SMALL, seed=3)
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_body_matches_float_reference(small_model, M):
+    print(f"step body M={M}", flush=True)
+    m = small_model
+    g = torch.Generator(device="cuda:0").manual_seed(M)
+    x0 = torch.randn(M, m.cfg.hidden, device="cuda:0", generator=g).to(torch.bfloat16)
+    got = m.body(x0).float()
+    ref = _ref_body(m, x0)
+    rel = ((got - ref).norm() / ref.norm()).item()
+    assert rel < 2e-2, rel
+
+
+def test_step_accept_and_graph_replay(small_model):
+    from tokenrush_amd.accept import AcceptState
+    print("step graph", flush=True)
+    m = small_model
+    M = 8
+    g = torch.Generator(device="cuda:0").manual_seed(11)
+    x0 = torch.randn(M, m.cfg.hidden, device="cuda:0", generator=g).to(torch.bfloat16)
+    st = AcceptState(M, "cuda:0")
+    # drafts: the target's own argmax on a prefix of 3, then a wrong token
+    logits = m.body(x0)
+    pred = logits.float().argmax(-1).cpu().numpy()
+    spec = np.zeros(M, dtype=np.int64)
+    spec[0] = 7
+    spec[1:4] = pred[0:3]
+    spec[4:] = (pred[3:7] + 1) % m.cfg.vocab
+    spec_t = torch.from_numpy(spec).to("cuda:0")
+    st.pos.fill_(100)
+    lg = m.step(x0, spec_t, st)
+    torch.cuda.synchronize()
+    lg_np = lg.view(torch.int16).cpu().numpy().view(np.uint16)
+    want = oa.verify_chain(oa.argmax_rows(oa.logits_f32(lg_np)), spec, pos=100)
+    assert int(st.n_accepted) == want["n"] >= 3 and int(st.tok) == want["tok"] and int(st.pos) == want["pos"]
+    eager = (lg.clone(), st.n_accepted.clone(), st.tok.clone(), st.slot.clone(), st.tokens.clone(), st.commit.clone())
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        st.pos.fill_(100)
+        m.step(x0, spec_t, st)                     # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        lg_g = m.step(x0, spec_t, st)
+    for rep in range(3):
+        st.pos.fill_(100)
+        st.n_accepted.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        _ = m.body(x0)                              # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(lg_g, eager[0]), rep
+        assert torch.equal(st.n_accepted, eager[1]) and torch.equal(st.tok, eager[2]), rep
+        assert torch.equal(st.slot, eager[3]) and torch.equal(st.tokens, eager[4]) and torch.equal(st.commit, eager[5])
+        assert int(st.pos) == want["pos"]

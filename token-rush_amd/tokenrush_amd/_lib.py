@@ -40,6 +40,8 @@ SIGNATURES = {
     "tr_accept_sample": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tr_accept_residual": (_I, [_P, _I, _I, _P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P]),
     "tr_commit_rows": (_I, [_P, _I, ctypes.c_long, _I, _P, _P, _P, _I, _P]),
+    "tr_add_rmsnorm": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _I, ctypes.c_float, _I, _P]),
+    "tr_silu_mul": (_I, [_P, ctypes.c_long, _P, _I, _I, _P]),
 }
 
 _lib = None
