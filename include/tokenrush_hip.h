@@ -149,12 +149,14 @@ int tr_commit_rows(void* data, int planes, long plane_stride_bytes, int row_byte
 /* Split-K partial consumer: x [T, N] bf16, h per h_mode (0 none, 1 bf16 [T, N], 2 fp32 partials
  * [n_slots, T, N] summed in slot order then rounded to bf16), weight [N] bf16 ->
  * xo = bf16(x + h) (not written when h_mode is 0) and y = rmsnorm(xo) * (1 + weight), or
- * bf16(weight * bf16(rmsnorm(xo))) when plain. N <= 8192; one workgroup per row.
+ * bf16(weight * bf16(rmsnorm(xo))) when plain. N % 8 == 0, N <= 8192, n_slots <= 8; one
+ * workgroup per row; x, h, weight, xo, y 16-byte aligned.
  * Replaces: add_rmsnorm (tokenrush/fused.py:23-60). */
 int tr_add_rmsnorm(const void* x, const void* h, int h_mode, int n_slots, const void* weight, void* xo, void* y,
                    int T, int N, float eps, int plain, void* stream);
 
 /* gate_up [T, 2F] bf16 (rows ld >= 2F elements apart; 0 = 2F) -> y [T, F] bf16 = silu(gate) * up.
+ * F % 8 == 0, ld % 8 == 0, pointers 16-byte aligned.
  * Replaces: silu_mul (tokenrush/fused.py:67-87). */
 int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* stream);
 

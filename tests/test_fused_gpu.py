@@ -28,7 +28,7 @@ def _ulp_close(got, ref, ulps=1):
     assert np.all(np.abs(got - ref) <= ulps * 2.0 ** (e - 7) + 1e-30), np.abs(got - ref).max()
 
 
-@pytest.mark.parametrize("T,N,S", [(1, 5120, 1), (8, 5120, 3), (8, 5120, 1), (32, 5120, 4), (5, 1000, 2), (3, 8192, 6)])
+@pytest.mark.parametrize("T,N,S", [(1, 5120, 1), (8, 5120, 3), (8, 5120, 1), (32, 5120, 4), (5, 1000, 2), (3, 8192, 6), (2, 8, 8)])
 def test_add_rmsnorm_partials(dev, T, N, S):
     from tokenrush_amd.fused import add_rmsnorm
     print(f"add_rmsnorm T={T} N={N} S={S}", flush=True)
@@ -60,7 +60,7 @@ def test_add_rmsnorm_modes_and_presum(dev):
     _ulp_close(yp, yp_r, ulps=2)
 
 
-@pytest.mark.parametrize("T,F", [(1, 17408), (8, 17408), (32, 1000)])
+@pytest.mark.parametrize("T,F", [(1, 17408), (8, 17408), (32, 1000), (3, 8)])
 def test_silu_mul(dev, T, F):
     from tokenrush_amd.fused import silu_mul
     rng = np.random.default_rng(F + T)

@@ -6,7 +6,8 @@
 //         (or h given as bf16, or no h)
 //   x'  = bf16(x + h)            the residual stream, written to xo
 //   y   = x' * rsqrt(mean(x'^2) + eps) * (1 + w)      (plain: bf16(w * bf16(x' * rsqrt(...))))
-// One workgroup per row; the row stays in registers between the two passes.
+// One workgroup per row, 8 elements per thread in registers between the two passes; N % 8 == 0,
+// N <= 8192, at most 8 partial slots.
 //
 // silu_mul (tokenrush/fused.py:67-87): y[t, i] = silu(gate[t, i]) * up[t, i] with gate_up[t] =
 // [gate (F) | up (F)] (rows ld elements apart), fp32 arithmetic, bf16 out.
@@ -14,10 +15,13 @@
 
 namespace tr {
 
-constexpr int kNormThreads = 1024;
-constexpr int kNormPerThread = 8;  // N <= 8192
+constexpr int kRowVec = 8;          // elements per thread: one 16-byte bf16 load
+constexpr int kMaxRowThreads = 1024;
+constexpr int kMaxSlots = 8;        // split-K slots the consumer sums (the GEMM makes <= 4 here)
 
 enum { H_NONE = 0, H_BF16 = 1, H_PARTIALS = 2 };
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float block_sum(float v, float* sh) {
 #pragma unroll
@@ -31,66 +35,108 @@ __device__ __forceinline__ float block_sum(float v, float* sh) {
   return t;
 }
 
-__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, const void* h,
-                                                                   int h_mode, int S, const uint16_t* __restrict__ w,
-                                                                   uint16_t* xo, uint16_t* __restrict__ y, int T, int N,
-                                                                   float eps, int plain) {
-  __shared__ float sh[kNormThreads / 64];
-  const int t = blockIdx.x;
-  float v[kNormPerThread];
-  float ss = 0.f;
+__device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-  for (int j = 0; j < kNormPerThread; ++j) {
-    const int i = threadIdx.x + j * blockDim.x;
-    float xv = 0.f;
-    if (i < N) {
-      xv = bf16_bits_to_f32(x[(size_t)t * N + i]);
-      if (h_mode != H_NONE) {
-        float hv;
-        if (h_mode == H_BF16) {
-          hv = bf16_bits_to_f32(((const uint16_t*)h)[(size_t)t * N + i]);
-        } else {
-          const float* p = (const float*)h;
-          hv = p[(size_t)t * N + i];
-          for (int s = 1; s < S; ++s) hv += p[((size_t)s * T + t) * N + i];
-          hv = bf16_bits_to_f32(f32_to_bf16_bits(hv));
-        }
-        xv = bf16_bits_to_f32(f32_to_bf16_bits(xv + hv));  // the residual stream is bf16
-        xo[(size_t)t * N + i] = f32_to_bf16_bits(xv);
-      }
-    }
-    v[j] = xv;
-    ss = fmaf(xv, xv, ss);
-  }
-  const float var = block_sum(ss, sh) / (float)N;
-  const float r = 1.0f / sqrtf(var + eps);
-#pragma unroll
-  for (int j = 0; j < kNormPerThread; ++j) {
-    const int i = threadIdx.x + j * blockDim.x;
-    if (i >= N) continue;
-    const float wv = bf16_bits_to_f32(w[i]);
-    float out;
-    if (plain)
-      out = wv * bf16_bits_to_f32(f32_to_bf16_bits(v[j] * r));  // Qwen3: cast, then weight * x
-    else
-      out = v[j] * r * (1.0f + wv);                             // Qwen3.5: gain is 1 + weight
-    y[(size_t)t * N + i] = f32_to_bf16_bits(out);
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_bits_to_f32(w[i] & 0xFFFFu);
+    f[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
   }
 }
 
-__global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, long ld, uint16_t* __restrict__ y, int T, int F) {
-  const size_t total = (size_t)T * F;
-  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < total; e += (size_t)gridDim.x * blockDim.x) {
-    const size_t t = e / F, i = e % F;
-    const float g = bf16_bits_to_f32(gu[t * ld + i]);
-    const float u = bf16_bits_to_f32(gu[t * ld + F + i]);
-    y[e] = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f32_to_bf16_bits(f[2 * i]) | ((uint32_t)f32_to_bf16_bits(f[2 * i + 1]) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// One workgroup per row, 8 consecutive elements per thread, every load of the row (x and all S
+// partial slots) issued before any arithmetic.
+template <int HM, int S>
+__global__ __launch_bounds__(kMaxRowThreads) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, const void* h,
+                                                                     const uint16_t* __restrict__ w, uint16_t* xo,
+                                                                     uint16_t* __restrict__ y, int T, int N, float eps,
+                                                                     int plain) {
+  __shared__ float sh[kMaxRowThreads / 64];
+  const int t = blockIdx.x;
+  const int i0 = threadIdx.x * kRowVec;
+  const bool on = i0 < N;
+  const size_t row = (size_t)t * N + i0;
+  float v[kRowVec];
+  uint4 xv = make_uint4(0, 0, 0, 0), hv = xv;
+  float4 part[S > 0 ? S : 1][2];
+#pragma unroll
+  for (int s = 0; s < (S > 0 ? S : 1); ++s) part[s][0] = part[s][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (on) {
+    xv = *(const uint4*)(x + row);
+    if (HM == H_BF16) hv = *(const uint4*)((const uint16_t*)h + row);
+    if (HM == H_PARTIALS) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const float4* p = (const float4*)((const float*)h + ((size_t)s * T + t) * N + i0);
+        part[s][0] = p[0];
+        part[s][1] = p[1];
+      }
+    }
   }
+  unpack8(xv, v);
+  if (HM != H_NONE) {
+    float hf[kRowVec];
+    if (HM == H_BF16) {
+      unpack8(hv, hf);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kRowVec; ++e) {
+        float acc = e < 4 ? part[0][0][e] : part[0][1][e - 4];
+#pragma unroll
+        for (int s = 1; s < S; ++s) acc += e < 4 ? part[s][0][e] : part[s][1][e - 4];  // slot order
+        hf[e] = bf16_bits_to_f32(f32_to_bf16_bits(acc));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kRowVec; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] + hf[e]));  // bf16 residual
+    if (on) *(uint4*)(xo + row) = pack8(v);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < kRowVec; ++e) ss = fmaf(v[e], v[e], ss);
+  const float r = 1.0f / sqrtf(block_sum(ss, sh) / (float)N + eps);
+  if (!on) return;
+  float wf[kRowVec], out[kRowVec];
+  unpack8(*(const uint4*)(w + i0), wf);
+#pragma unroll
+  for (int e = 0; e < kRowVec; ++e)
+    out[e] = plain ? wf[e] * bf16_bits_to_f32(f32_to_bf16_bits(v[e] * r))  // Qwen3: cast, then weight * x
+                   : v[e] * r * (1.0f + wf[e]);                              // Qwen3.5: gain is 1 + weight
+  *(uint4*)(y + row) = pack8(out);
+}
+
+// Grid (F / (8 * blockDim), T): 8 consecutive elements per thread.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, long ld, uint16_t* __restrict__ y,
+                                                       int F) {
+  const int t = blockIdx.y;
+  const int i0 = (blockIdx.x * blockDim.x + threadIdx.x) * kRowVec;
+  if (i0 >= F) return;
+  float g[kRowVec], u[kRowVec], out[kRowVec];
+  unpack8(*(const uint4*)(gu + (size_t)t * ld + i0), g);
+  unpack8(*(const uint4*)(gu + (size_t)t * ld + F + i0), u);
+#pragma unroll
+  for (int e = 0; e < kRowVec; ++e) out[e] = g[e] / (1.0f + __expf(-g[e])) * u[e];
+  *(uint4*)(y + (size_t)t * F + i0) = pack8(out);
 }
 
 }  // namespace tr
 
 using namespace tr;
+
+template <int HM, int S>
+static hipError_t launch_norm(dim3 grid, dim3 block, hipStream_t st, const void* x, const void* h, const void* w,
+                              void* xo, void* y, int T, int N, float eps, int plain) {
+  hipLaunchKernelGGL((add_rmsnorm_kernel<HM, S>), grid, block, 0, st, (const uint16_t*)x, h, (const uint16_t*)w,
+                     (uint16_t*)xo, (uint16_t*)y, T, N, eps, plain);
+  return hipGetLastError();
+}
 
 extern "C" {
 
@@ -98,24 +144,39 @@ int tr_add_rmsnorm(const void* x, const void* h, int h_mode, int n_slots, const 
                    int T, int N, float eps, int plain, void* stream) {
   if (!x || !weight || !y) return TR_ERR_ARG;
   if (h_mode < H_NONE || h_mode > H_PARTIALS || (h_mode != H_NONE && (!h || !xo))) return TR_ERR_ARG;
-  if (h_mode == H_PARTIALS && n_slots < 1) return TR_ERR_ARG;
-  if (T < 0 || N <= 0 || N > kNormThreads * kNormPerThread) return TR_ERR_SHAPE;
+  if (h_mode == H_PARTIALS && (n_slots < 1 || n_slots > kMaxSlots)) return TR_ERR_ARG;
+  if (T < 0 || N <= 0 || N % kRowVec || N > kMaxRowThreads * kRowVec) return TR_ERR_SHAPE;
   if (T == 0) return TR_OK;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, (hipStream_t)stream, (const uint16_t*)x, h,
-                     h_mode, n_slots, (const uint16_t*)weight, (uint16_t*)xo, (uint16_t*)y, T, N, eps, plain);
-  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+  const int threads = ((N / kRowVec + 63) / 64) * 64;
+  const dim3 grid(T), block(threads);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (h_mode == H_NONE) e = launch_norm<H_NONE, 0>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain);
+  else if (h_mode == H_BF16) e = launch_norm<H_BF16, 0>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain);
+  else {
+    switch (n_slots) {
+      case 1: e = launch_norm<H_PARTIALS, 1>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain); break;
+      case 2: e = launch_norm<H_PARTIALS, 2>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain); break;
+      case 3: e = launch_norm<H_PARTIALS, 3>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain); break;
+      case 4: e = launch_norm<H_PARTIALS, 4>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain); break;
+      case 5: e = launch_norm<H_PARTIALS, 5>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain); break;
+      case 6: e = launch_norm<H_PARTIALS, 6>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain); break;
+      case 7: e = launch_norm<H_PARTIALS, 7>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain); break;
+      default: e = launch_norm<H_PARTIALS, 8>(grid, block, st, x, h, weight, xo, y, T, N, eps, plain); break;
+    }
+  }
+  return e == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
 int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* stream) {
   if (!gate_up || !y) return TR_ERR_ARG;
-  if (T < 0 || F <= 0) return TR_ERR_SHAPE;
+  if (T < 0 || F <= 0 || F % kRowVec) return TR_ERR_SHAPE;
   if (ld == 0) ld = 2L * F;
-  if (ld < 2L * F) return TR_ERR_ARG;
+  if (ld < 2L * F || ld % kRowVec) return TR_ERR_ARG;
   if (T == 0) return TR_OK;
-  size_t blocks = ((size_t)T * F + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3((int)blocks), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)gate_up,
-                     ld, (uint16_t*)y, T, F);
+  const int per_block = 256 * kRowVec;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((F + per_block - 1) / per_block, T), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)gate_up, ld, (uint16_t*)y, F);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 

@@ -34,7 +34,7 @@
 // A wave reads one strip's four groups with four 16-byte loads per lane plus one 16-byte load
 // of parameters, all at one scalar offset.
 //
-// Work split ("activation-stationary"): a workgroup owns a range of strips and a K slot; each
+// Work split ("activation-stationary"): a workgroup owns every grid_n-th strip and a K slot; each
 // of its W waves owns one K block of GW groups (GW = 4 for M <= 16, 2 above), loads that
 // block's activations into registers once, then streams the strips' tiles for its block.
 // After every few strips the waves' partial tiles are summed through LDS in fixed wave order
@@ -178,8 +178,13 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int slot = blockIdx.x % a.S;
   const int rbi = blockIdx.x / a.S;
-  const int r0 = rbi * a.R;
-  const int r1 = min(nstrips, r0 + a.R);
+  // Workgroup rbi of the grid_n row workgroups takes strips rbi, rbi + grid_n, ...: at any
+  // moment all workgroups stream one contiguous band of the weight, which keeps their progress
+  // even (contiguous per-workgroup ranges finish up to 3 us apart on the large shapes).
+  const int gn = gridDim.x / a.S;
+  const int r0 = 0;
+  const int r1 = (nstrips - rbi + gn - 1) / gn;
+  auto phys = [&](int r) { return rbi + r * gn; };
 
   const int nb = Gp / GW;                              // K blocks (GW divides a quad)
   const int b0 = (int)(((long)slot * nb) / a.S), b1 = (int)(((long)(slot + 1) * nb) / a.S);
@@ -195,7 +200,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   const int quad_stride = Gp / kQuad * kQuadBytes;
   const int blk_off = gbase / kQuad * kQuadBytes + gbase % kQuad * kCodeBytes;
   const int oob = nstrips * quad_stride;
-  auto strip_off = [&](int r) { return __builtin_amdgcn_readfirstlane(r < r1 ? r * quad_stride + blk_off : oob); };
+  auto strip_off = [&](int r) { return __builtin_amdgcn_readfirstlane(r < r1 ? phys(r) * quad_stride + blk_off : oob); };
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.packed, (short)0, oob, 0x00020000);
   const int lane_off = 16 * lane;
   // parameters of row lane % 16, groups gbase % 4 .. + GW - 1, relative to the strip offset
@@ -288,7 +293,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int w = 0; w < kMaxWaves; ++w)
               if (w < nw) v += part[w];
-            const int n = 16 * (r_first + sidx) + n16;
+            const int n = 16 * phys(r_first + sidx) + n16;
             if (a.mode == OUT_BF16)
               ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
             else if (a.mode == OUT_PARTIAL)
@@ -321,7 +326,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   if (!last) return;
   const int cols = (r1 - r0) * 16;
   for (int e = threadIdx.x; e < a.M * cols; e += blockDim.x) {
-    const int m = e / cols, n = r0 * 16 + e % cols;
+    const int m = e / cols, n = 16 * phys(r0 + (e % cols) / 16) + e % 16;
     float v = 0.f;
     for (int s = 0; s < a.S; ++s)
       v += __hip_atomic_load(a.ws_part + ((size_t)s * a.M + m) * a.N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
