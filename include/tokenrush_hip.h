@@ -55,6 +55,13 @@ int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials
                     size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
                     int R, void* stream);
 
+/* Fused gate/up + activation: packed is a [gate (N/2 rows); up (N/2 rows)] weight packed by
+ * tr_pack_int4_pairs; out bf16 [M, N/2] = silu(bf16(x . gate^T)) * bf16(x . up^T), bit for bit what
+ * tr_int4_gemm followed by tr_silu_mul produce. N % 32 == 0; workspace as for tr_int4_gemm.
+ * Replaces: silu_mul(gate_up(n)) (tokenrush/model.py:156-160, tokenrush/fused.py:67-87) in one launch. */
+int tr_int4_gemm_silu(const void* x, const void* packed, void* out, void* workspace, size_t workspace_bytes, int M,
+                      int N, int K, int group, int scale_dtype, void* stream);
+
 /* The default tiling of an N x K weight for M rows: S K-slots, W waves and R strips per
  * workgroup. Depends on M only through M > 16. Host only, no GPU call. */
 int tr_gemm_plan(int N, int K, int M, int* S, int* W, int* R);
@@ -78,6 +85,14 @@ size_t tr_packed_bytes(int N, int K);
 int tr_pack_int4(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K,
                  void* stream);
 int tr_unpack_int4(const void* packed, void* qweight, void* scale, void* mn, int N, int K, void* stream);
+
+/* The same for a [gate; up] weight (N % 32 == 0) in the pair layout: packed strip s holds gate rows
+ * 8s..8s+7 then up rows 8s..8s+7 (engine rows 8s.., N/2 + 8s..). tr_int4_gemm on such a weight
+ * writes output column 16 s + i for engine row 8 s + i (i < 8) or N/2 + 8 s + i - 8.
+ * No counterpart in the reference (its gate/up output is a plain [gate | up] row, model.py:156). */
+int tr_pack_int4_pairs(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K,
+                       void* stream);
+int tr_unpack_int4_pairs(const void* packed, void* qweight, void* scale, void* mn, int N, int K, void* stream);
 
 /* Dense weight [N, K] in the scale dtype: round(round(q*s) + m), two roundings.
  * Replaces: dequantize_int4 (tokenrush/quant.py:47-53). */

@@ -227,3 +227,43 @@ def test_qlinear_api(dev):
     y = lin(dev_x(xl)).float().cpu().numpy()
     r = o.gemm_dequant(xl, p, s, m)
     assert np.abs(y - r).max() <= np.abs(r).max() * 2 ** -7
+
+
+@pytest.mark.parametrize("N,K", [(2048, 5120), (34816, 5120), (1024, 17408), (512, 384)])
+@pytest.mark.parametrize("M", [1, 8, 24])
+def test_gate_up_pair_layout_and_fused_silu(dev, N, K, M):
+    """Pair layout: byte-exact against the oracle's quad layout of the row-permuted weight, a
+    round trip through unpack, the plain product unchanged after unpair, and the fused silu
+    epilogue bit-identical to the product followed by the activation kernel (incl. K split
+    across workgroups, K = 17408)."""
+    from tokenrush_amd import gfx950
+    from tokenrush_amd.fused import silu_mul
+    say(f"pairs N={N} K={K} M={M}")
+    p, s, m = o.make_weights(N, K, seed=21, dtype="bf16")
+    qd, sd, md = dev_weights(p, s, m, "bf16")
+    Bp, sp, mp = gfx950.pack(qd, sd, md, pairs=True)
+    F = N // 2
+    perm = np.array([(8 * (r // 16) + r % 16) if r % 16 < 8 else F + 8 * (r // 16) + r % 16 - 8 for r in range(N)])
+    if M == 1:
+        assert np.array_equal(Bp.cpu().numpy(), o.pack_quads(p[perm], s[perm], m[perm], "bf16"))
+        q2, s2, m2 = gfx950.unpack(Bp, sp, mp, K, pairs=True)
+        assert torch.equal(q2, qd) and torch.equal(s2, sd) and torch.equal(m2, md)
+    B, sb, _ = gfx950.pack(qd, sd, md)
+    x = dev_x(o.make_x(M, K, seed=22))
+    y = gfx950.mul(x, B, sb)
+    assert torch.equal(gfx950.unpair(gfx950.mul(x, Bp, sp)), y)
+    assert torch.equal(gfx950.mul_silu(x, Bp, sp), silu_mul(y))
+
+
+def test_qlinear_gate_up_layout(dev):
+    from tokenrush_amd.fused import silu_mul
+    from tokenrush_amd.quant import QLinear
+    p, s, m = o.make_weights(1024, 1024, seed=23, dtype="bf16")
+    qd, sd, md = dev_weights(p, s, m, "bf16")
+    plain, gu = QLinear(qd, sd, md), QLinear(qd, sd, md, layout="gate_up")
+    x = dev_x(o.make_x(8, 1024, seed=24))
+    assert torch.equal(gu(x), plain(x))
+    assert torch.equal(gu.silu_mul(x), silu_mul(plain(x)))
+    q2, s2, m2 = gu.nibbles()
+    assert torch.equal(q2, qd) and torch.equal(s2, sd) and torch.equal(m2, md)
+    check_close(gu(x), o.gemm_exact(o.make_x(8, 1024, seed=24), p, s, m), "gate_up layout")

@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   unpack8(*(const uint4*)(gu + (size_t)t * ld + i0), g);
   unpack8(*(const uint4*)(gu + (size_t)t * ld + F + i0), u);
 #pragma unroll
-  for (int e = 0; e < kRowVec; ++e) out[e] = g[e] / (1.0f + __expf(-g[e])) * u[e];
+  for (int e = 0; e < kRowVec; ++e) out[e] = silu_mul_f32(g[e], u[e]);
   *(uint4*)(y + (size_t)t * F + i0) = pack8(out);
 }
 

@@ -163,6 +163,7 @@ struct GemmArgs {
   int M, N, K, S, R;      // R = strips per workgroup
   int RB;                 // strips per LDS reduction batch
   int mode;
+  int silu;               // 1: gate/up pair layout, out = silu(gate) * up, bf16 [M, N / 2]
 };
 
 // One accumulator tile element: (mt, lane, r) -> output row m = 16 mt + 4 (lane / 16) + r,
@@ -280,10 +281,9 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
         }
         if (sib == RB - 1 || r == r1 - 1) {
           __syncthreads();
-          const int ns = sib + 1, r_first = r - sib, per = a.M * 16;
-          for (int e = threadIdx.x; e < ns * per; e += blockDim.x) {
-            const int sidx = e / per, rem = e % per;
-            const int m = rem >> 4, n16 = rem & 15;
+          const int ns = sib + 1, r_first = r - sib;
+          // Sum over the nw waves' partial tiles, in wave order, of output (m, n16) of strip r_first + sidx.
+          auto wave_sum = [&](int sidx, int m, int n16) {
             const int mt = m >> 4, mm = m & 15;
             const float* src = ring + ((size_t)sidx * W * MT + mt) * 256 + (16 * (mm >> 2) + n16) * 4 + (mm & 3);
             float part[kMaxWaves];
@@ -293,14 +293,32 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int w = 0; w < kMaxWaves; ++w)
               if (w < nw) v += part[w];
-            const int n = 16 * phys(r_first + sidx) + n16;
-            if (a.mode == OUT_BF16)
-              ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
-            else if (a.mode == OUT_PARTIAL)
-              ((float*)a.out)[((size_t)slot * a.M + m) * a.N + n] = v;
-            else  // agent-scope store: written through to the coherence point, no L2 flush needed
-              __hip_atomic_store(a.ws_part + ((size_t)slot * a.M + m) * a.N + n, v, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+            return v;
+          };
+          if (a.silu && a.mode == OUT_BF16) {
+            // pair layout: rows 0..7 of a strip are gate rows, 8..15 the matching up rows
+            const int per = a.M * 8, F = a.N / 2;
+            for (int e = threadIdx.x; e < ns * per; e += blockDim.x) {
+              const int sidx = e / per, rem = e % per, m = rem >> 3, j = rem & 7;
+              const float g = bf16_bits_to_f32(f32_to_bf16_bits(wave_sum(sidx, m, j)));
+              const float u = bf16_bits_to_f32(f32_to_bf16_bits(wave_sum(sidx, m, j + 8)));
+              ((uint16_t*)a.out)[(size_t)m * F + 8 * phys(r_first + sidx) + j] = f32_to_bf16_bits(silu_mul_f32(g, u));
+            }
+          } else {
+            const int per = a.M * 16;
+            for (int e = threadIdx.x; e < ns * per; e += blockDim.x) {
+              const int sidx = e / per, rem = e % per;
+              const int m = rem >> 4, n16 = rem & 15;
+              const float v = wave_sum(sidx, m, n16);
+              const int n = 16 * phys(r_first + sidx) + n16;
+              if (a.mode == OUT_BF16)
+                ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
+              else if (a.mode == OUT_PARTIAL)
+                ((float*)a.out)[((size_t)slot * a.M + m) * a.N + n] = v;
+              else  // agent-scope store: written through to the coherence point, no L2 flush needed
+                __hip_atomic_store(a.ws_part + ((size_t)slot * a.M + m) * a.N + n, v, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
           }
           sib = 0;
           half ^= 1;
@@ -324,13 +342,26 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
            a.S - 1;
   __syncthreads();
   if (!last) return;
-  const int cols = (r1 - r0) * 16;
-  for (int e = threadIdx.x; e < a.M * cols; e += blockDim.x) {
-    const int m = e / cols, n = 16 * phys(r0 + (e % cols) / 16) + e % 16;
+  auto slot_sum = [&](int m, int n) {
     float v = 0.f;
     for (int s = 0; s < a.S; ++s)
       v += __hip_atomic_load(a.ws_part + ((size_t)s * a.M + m) * a.N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
+    return v;
+  };
+  if (a.silu) {
+    const int cols = (r1 - r0) * 8, F = a.N / 2;
+    for (int e = threadIdx.x; e < a.M * cols; e += blockDim.x) {
+      const int m = e / cols, strip = phys(r0 + (e % cols) / 8), j = e % 8;
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(slot_sum(m, 16 * strip + j)));
+      const float u = bf16_bits_to_f32(f32_to_bf16_bits(slot_sum(m, 16 * strip + j + 8)));
+      ((uint16_t*)a.out)[(size_t)m * F + 8 * strip + j] = f32_to_bf16_bits(silu_mul_f32(g, u));
+    }
+  } else {
+    const int cols = (r1 - r0) * 16;
+    for (int e = threadIdx.x; e < a.M * cols; e += blockDim.x) {
+      const int m = e / cols, n = 16 * phys(r0 + (e % cols) / 16) + e % 16;
+      ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(slot_sum(m, n));
+    }
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(a.ws_cnt + rbi * kWsCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -341,8 +372,14 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 // Engine packing (uint8 [N, K/2], element 2j in the low nibble of byte j; tokenrush/quant.py:9-10)
 // plus scale/min [N, K/128] -> quad layout. One thread per output 32-bit word (1088 per quad);
 // padding groups are written as zeros.
+// Engine row of packed row i (0..15) of strip `strip`: identity, or for the gate/up pair layout
+// (F = N / 2 > 0) gate row 8 strip + i for i < 8 and up row F + 8 strip + i - 8 otherwise.
+__host__ __device__ __forceinline__ size_t src_row(size_t strip, int i, int F) {
+  return F > 0 ? (i < 8 ? 8 * strip + i : (size_t)F + 8 * strip + (i - 8)) : 16 * strip + i;
+}
+
 __global__ void pack_kernel(const uint32_t* __restrict__ q, const uint16_t* __restrict__ scale,
-                            const uint16_t* __restrict__ mn, uint32_t* __restrict__ packed, int N, int K) {
+                            const uint16_t* __restrict__ mn, uint32_t* __restrict__ packed, int N, int K, int F) {
   const int G = K / kGroup, nq = padded_groups(K) / kQuad;
   constexpr int kWords = kQuadBytes / 4;
   const size_t total = (size_t)N / 16 * nq * kWords;
@@ -353,7 +390,7 @@ __global__ void pack_kernel(const uint32_t* __restrict__ q, const uint16_t* __re
     const int q0 = (int)(quad % nq) * kQuad;
     if (d >= kSmOff / 4) {
       const int e = d - kSmOff / 4, g = q0 + (e & 3);
-      const size_t n = strip * 16 + (e >> 2);
+      const size_t n = src_row(strip, e >> 2, F);
       packed[i] = g < G ? (uint32_t)scale[n * G + g] | ((uint32_t)mn[n * G + g] << 16) : 0u;
       continue;
     }
@@ -362,7 +399,7 @@ __global__ void pack_kernel(const uint32_t* __restrict__ q, const uint16_t* __re
       packed[i] = 0u;
       continue;
     }
-    const size_t n = strip * 16 + (lane & 15);
+    const size_t n = src_row(strip, lane & 15, F);
     const int k0 = g * kGroup + 32 * j + 8 * (lane >> 4);
     const uint32_t u = q[(n * K + k0) / 8];  // bytes b0..b3 = codes k0..k0+7
     uint32_t w = 0;
@@ -378,7 +415,7 @@ __global__ void pack_kernel(const uint32_t* __restrict__ q, const uint16_t* __re
 
 // Quad layout -> engine packing and scale/min (the inverse of pack_kernel; padding is dropped).
 __global__ void unpack_kernel(const uint32_t* __restrict__ packed, uint32_t* __restrict__ q,
-                              uint16_t* __restrict__ scale, uint16_t* __restrict__ mn, int N, int K) {
+                              uint16_t* __restrict__ scale, uint16_t* __restrict__ mn, int N, int K, int F) {
   const int G = K / kGroup, nq = padded_groups(K) / kQuad;
   constexpr int kWords = kQuadBytes / 4;
   const size_t total = (size_t)N / 16 * nq * kWords;
@@ -391,14 +428,14 @@ __global__ void unpack_kernel(const uint32_t* __restrict__ packed, uint32_t* __r
     if (d >= kSmOff / 4) {
       const int e = d - kSmOff / 4, g = q0 + (e & 3);
       if (g >= G) continue;
-      const size_t n = strip * 16 + (e >> 2);
+      const size_t n = src_row(strip, e >> 2, F);
       scale[n * G + g] = (uint16_t)(w & 0xFFFF);
       mn[n * G + g] = (uint16_t)(w >> 16);
       continue;
     }
     const int g = q0 + d / 256, j = d & 3, lane = (d & 255) >> 2;
     if (g >= G) continue;
-    const size_t n = strip * 16 + (lane & 15);
+    const size_t n = src_row(strip, lane & 15, F);
     const int k0 = g * kGroup + 32 * j + 8 * (lane >> 4);
     uint32_t u = 0;
 #pragma unroll
@@ -548,11 +585,13 @@ size_t tr_gemm_workspace_bytes(int N, int K, int M) {
   return ws_counter_bytes() + (size_t)p.S * M * N * sizeof(float);
 }
 
-int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials, void* workspace,
-                    size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots, int R,
-                    void* stream) {
+static int gemm_impl(const void* x, const void* packed, void* out, void* partials, void* workspace,
+                     size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots, int R,
+                     int silu, void* stream) {
   if (group != kGroup) return TR_ERR_CONFIG;
   if (M < 0 || M > 32 || !shape_ok(N, K)) return TR_ERR_SHAPE;
+  if (silu && partials) return TR_ERR_ARG;
+  if (silu && N % 32) return TR_ERR_SHAPE;
   if (M == 0) return TR_OK;
   if (!x || !packed || (!out == !partials)) return TR_ERR_ARG;
   if (scale_dtype != 0 && scale_dtype != 1) return TR_ERR_ARG;
@@ -569,6 +608,7 @@ int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials
   a.R = p.R;
   a.ws_part = nullptr;
   a.ws_cnt = nullptr;
+  a.silu = silu;
   if (partials) {
     a.mode = OUT_PARTIAL;
     a.out = partials;
@@ -587,6 +627,18 @@ int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials
   return launch(a, p, scale_dtype, (hipStream_t)stream) == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
+int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials, void* workspace,
+                    size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots, int R,
+                    void* stream) {
+  return gemm_impl(x, packed, out, partials, workspace, workspace_bytes, M, N, K, group, scale_dtype, n_slots, R, 0,
+                   stream);
+}
+
+int tr_int4_gemm_silu(const void* x, const void* packed, void* out, void* workspace, size_t workspace_bytes, int M,
+                      int N, int K, int group, int scale_dtype, void* stream) {
+  return gemm_impl(x, packed, out, nullptr, workspace, workspace_bytes, M, N, K, group, scale_dtype, 0, 0, 1, stream);
+}
+
 int tr_int4_gemm(const void* x, const void* packed, void* out, void* partials, void* workspace,
                  size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
                  void* stream) {
@@ -601,22 +653,40 @@ static int grid_for(size_t work) {
   return (int)b;
 }
 
-int tr_pack_int4(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K, void* stream) {
+static int pack_impl(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K, int F,
+                     void* stream) {
   if (!qweight || !scale || !mn || !packed) return TR_ERR_ARG;
-  if (!shape_ok(N, K)) return TR_ERR_SHAPE;
+  if (!shape_ok(N, K) || (F && N % 32)) return TR_ERR_SHAPE;
   const size_t total = packed_bytes(N, K) / 4;
   hipLaunchKernelGGL(pack_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, (const uint32_t*)qweight,
-                     (const uint16_t*)scale, (const uint16_t*)mn, (uint32_t*)packed, N, K);
+                     (const uint16_t*)scale, (const uint16_t*)mn, (uint32_t*)packed, N, K, F);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
-int tr_unpack_int4(const void* packed, void* qweight, void* scale, void* mn, int N, int K, void* stream) {
+static int unpack_impl(const void* packed, void* qweight, void* scale, void* mn, int N, int K, int F, void* stream) {
   if (!qweight || !packed || !scale || !mn) return TR_ERR_ARG;
-  if (!shape_ok(N, K)) return TR_ERR_SHAPE;
+  if (!shape_ok(N, K) || (F && N % 32)) return TR_ERR_SHAPE;
   const size_t total = packed_bytes(N, K) / 4;
   hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint32_t*)packed, (uint32_t*)qweight, (uint16_t*)scale, (uint16_t*)mn, N, K);
+                     (const uint32_t*)packed, (uint32_t*)qweight, (uint16_t*)scale, (uint16_t*)mn, N, K, F);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+int tr_pack_int4(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K, void* stream) {
+  return pack_impl(qweight, scale, mn, packed, N, K, 0, stream);
+}
+
+int tr_unpack_int4(const void* packed, void* qweight, void* scale, void* mn, int N, int K, void* stream) {
+  return unpack_impl(packed, qweight, scale, mn, N, K, 0, stream);
+}
+
+int tr_pack_int4_pairs(const void* qweight, const void* scale, const void* mn, void* packed, int N, int K,
+                       void* stream) {
+  return pack_impl(qweight, scale, mn, packed, N, K, N / 2, stream);
+}
+
+int tr_unpack_int4_pairs(const void* packed, void* qweight, void* scale, void* mn, int N, int K, void* stream) {
+  return unpack_impl(packed, qweight, scale, mn, N, K, N / 2, stream);
 }
 
 int tr_dequant_int4(const void* qweight, const void* scale, const void* mn, void* out, int N, int K, int group,

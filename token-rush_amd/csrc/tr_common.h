@@ -35,6 +35,10 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
 }
 
+// silu(g) * u in fp32, the MLP activation (tokenrush/fused.py:76). One definition for the fused
+// GEMM epilogue and the stand-alone kernel, so the two paths agree bit for bit.
+__device__ __forceinline__ float silu_mul_f32(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+
 // A value the compiler must keep in a VGPR: lets v_and_or_b32 take (VGPR, SGPR, VGPR)
 // operands, since a gfx9 VOP3 instruction reads at most one scalar/literal.
 __device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {

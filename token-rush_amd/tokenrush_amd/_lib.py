@@ -29,8 +29,11 @@ SIGNATURES = {
     "tr_packed_bytes": (_S, [_I, _I]),
     "tr_int4_gemm": (_I, [_P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _I, _P]),
     "tr_int4_gemm_ex": (_I, [_P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "tr_int4_gemm_silu": (_I, [_P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P]),
     "tr_pack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "tr_unpack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "tr_pack_int4_pairs": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "tr_unpack_int4_pairs": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "tr_dequant_int4": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "tr_accept_workspace_bytes": (_S, [_I, _I]),
     "tr_argmax_rows": (_I, [_P, _I, _I, _P, _S, _P, _P]),

@@ -66,10 +66,12 @@ def _sm_views(B: torch.Tensor, dtype):
     return sm[..., 0], sm[..., 1]
 
 
-def pack(qweight: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor):
+def pack(qweight: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor, pairs: bool = False):
     """Engine packing (uint8 [N, K/2], bf16/fp16 [N, K/128] x2) -> (B, s, m): B is the quad
     layout uint8 [N/16, Gp/4, 4352] holding codes, scale and min; s and m are views into B
-    (they carry the scale dtype). The counterpart of marlin.pack (marlin.py:73-96)."""
+    (they carry the scale dtype). The counterpart of marlin.pack (marlin.py:73-96).
+    pairs: the weight is [gate; up] (N % 32 == 0); strip s holds gate rows 8s.. and up rows
+    N/2 + 8s.., the layout mul_silu needs."""
     _lib.require_gpu(qweight, scale, mn)
     N, K = qweight.shape[0], qweight.shape[1] * 2
     _check_shape(N, K)
@@ -78,13 +80,15 @@ def pack(qweight: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor):
     if scale.dtype not in SCALE_DTYPES or mn.dtype != scale.dtype:
         raise RuntimeError("scale/min must both be bf16 or fp16")
     q, s, m = qweight.contiguous(), scale.contiguous(), mn.contiguous()
+    if pairs and N % 32:
+        raise RuntimeError(f"pair layout needs n % 32 == 0, got n={N}")
     B = torch.empty(N // 16, padded_groups(K) // 4, QUAD, dtype=torch.uint8, device=q.device)
-    _lib.check(ext().tr_pack_int4(_lib.ptr(q), _lib.ptr(s), _lib.ptr(m), _lib.ptr(B), N, K, _lib.stream_of(q)),
-               "tr_pack_int4")
+    fn = ext().tr_pack_int4_pairs if pairs else ext().tr_pack_int4
+    _lib.check(fn(_lib.ptr(q), _lib.ptr(s), _lib.ptr(m), _lib.ptr(B), N, K, _lib.stream_of(q)), "tr_pack_int4")
     return (B,) + _sm_views(B, scale.dtype)
 
 
-def unpack(B: torch.Tensor, s: torch.Tensor, m: torch.Tensor, K: int = None):
+def unpack(B: torch.Tensor, s: torch.Tensor, m: torch.Tensor, K: int = None, pairs: bool = False):
     """Inverse of pack -> (qweight uint8 [N, K/2], scale [N, K/128], mn [N, K/128])
     (marlin.unpack, marlin.py:99-118). s only supplies the scale dtype. K defaults to the
     padded width; pass the true K when K/128 is not a multiple of 4."""
@@ -96,8 +100,8 @@ def unpack(B: torch.Tensor, s: torch.Tensor, m: torch.Tensor, K: int = None):
     q = torch.empty(N, K // 2, dtype=torch.uint8, device=B.device)
     sc = torch.empty(N, K // GROUP, dtype=s.dtype, device=B.device)
     mn = torch.empty_like(sc)
-    _lib.check(ext().tr_unpack_int4(_lib.ptr(B), _lib.ptr(q), _lib.ptr(sc), _lib.ptr(mn), N, K, _lib.stream_of(B)),
-               "tr_unpack_int4")
+    fn = ext().tr_unpack_int4_pairs if pairs else ext().tr_unpack_int4
+    _lib.check(fn(_lib.ptr(B), _lib.ptr(q), _lib.ptr(sc), _lib.ptr(mn), N, K, _lib.stream_of(B)), "tr_unpack_int4")
     return q, sc, mn
 
 
@@ -167,6 +171,33 @@ def mul(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor = Non
     strips_per_wg / slots override the tiling (0 / -1 = default)."""
     y = torch.empty(x.shape[0], B.shape[0] * 16, dtype=torch.bfloat16, device=x.device)
     _launch(x, B, s, y, False, 0, strips_per_wg, slots)
+    return y
+
+
+def unpair(y: torch.Tensor) -> torch.Tensor:
+    """Columns of a pair-layout product [..., N] (strip s: gate 8s..8s+7, up N/2 + 8s..) back to
+    the engine order [gate | up]."""
+    lead, N = y.shape[:-1], y.shape[-1]
+    return y.view(*lead, N // 16, 2, 8).transpose(-3, -2).reshape(*lead, N)
+
+
+def mul_silu(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor):
+    """x [M, K] bf16 (M <= 32), B a pair-layout [gate; up] weight -> silu(x . gate^T) * (x . up^T)
+    as bf16 [M, N/2] in one launch: the gate/up GEMM with the activation of
+    tokenrush/fused.py:67-87 in its epilogue (each product rounded to bf16 first)."""
+    M, K = x.shape
+    N = B.shape[0] * 16
+    if x.dtype != torch.bfloat16 or s.dtype not in SCALE_DTYPES or not (x.is_contiguous() and B.is_contiguous()):
+        raise RuntimeError("mul_silu: x must be contiguous bf16, scale/min bf16 or fp16")
+    if M > MAX_ROWS or K % GROUP or padded_groups(K) != B.shape[1] * 4 or B.shape[2] != QUAD or N % 32:
+        raise RuntimeError(f"problem shape (m={M}, n={N}, k={K}) not supported")
+    _lib.require_gpu(x, B)
+    y = torch.empty(M, N // 2, dtype=torch.bfloat16, device=x.device)
+    need = workspace_bytes(N, K, M)
+    ws, nbytes = (None, 0) if need == 0 else workspaces(N, x.device, K, M, min_bytes=need)
+    rc = ext().tr_int4_gemm_silu(_lib.ptr(x), _lib.ptr(B), _lib.ptr(y), _lib.ptr(ws), nbytes, M, N, K, GROUP,
+                                 SCALE_DTYPES[s.dtype], _lib.stream_of(x))
+    _lib.check(rc, f"tr_int4_gemm_silu (m={M}, n={N}, k={K})")
     return y
 
 

@@ -58,17 +58,20 @@ class QLinear:
     the hidden-sized outputs, weights.py:163-174); partials(x) then returns [S, T, N] with
     S = gfx950.partial_slots(N, K), whose sum over S is the product."""
 
-    def __init__(self, qweight, scale, mn, backend=DEFAULT_BACKEND, split_k: int = 1):
+    def __init__(self, qweight, scale, mn, backend=DEFAULT_BACKEND, split_k: int = 1, layout: str = "rows"):
         backend = _ALIASES.get(backend, backend)
         assert backend in BACKENDS, backend
+        assert layout in ("rows", "gate_up"), layout
         self.shape_ = (qweight.shape[0], qweight.shape[1] * 2)
         self.group = self.shape_[1] // scale.shape[1]
         self.backend = backend
         self.split_k = split_k
+        # "gate_up": the weight is [gate; up] and silu_mul(x) fuses the activation (gfx950 only)
+        self.layout = layout if backend == "gfx950" else "rows"
         if backend == "gfx950":
             if self.group != GROUP:
                 raise RuntimeError(f"gfx950 backend needs group {GROUP}, got {self.group}")
-            self.B, self.s, self.m = gfx950.pack(qweight, scale, mn)
+            self.B, self.s, self.m = gfx950.pack(qweight, scale, mn, pairs=self.layout == "gate_up")
             gfx950.workspaces(self.shape_[0], qweight.device, self.shape_[1])   # sized before any graph capture
             self.qweight = self.scale = self.mn = None
         else:
@@ -93,7 +96,7 @@ class QLinear:
     def nibbles(self):
         """(qweight, scale, mn) in the engine's packing (unpacked from the strip layout if needed)."""
         if self.backend == "gfx950":
-            return gfx950.unpack(self.B, self.s, self.m, self.shape_[1])
+            return gfx950.unpack(self.B, self.s, self.m, self.shape_[1], pairs=self.layout == "gate_up")
         return self.qweight, self.scale, self.mn
 
     def rows(self, ids: torch.Tensor):
@@ -107,7 +110,17 @@ class QLinear:
         T = x.shape[0]
         if self.backend == "dequant" or T > MAX_ROWS:
             return F.linear(x, self.dequantize().to(x.dtype))
-        return gfx950.mul(x.contiguous(), self.B, self.s)
+        y = gfx950.mul(x.contiguous(), self.B, self.s)
+        return gfx950.unpair(y) if self.layout == "gate_up" else y
+
+    def silu_mul(self, x: torch.Tensor) -> torch.Tensor:
+        """silu(gate) * up of this [gate; up] weight's product, [T, N/2] bf16: one fused launch
+        for a "gate_up" layout, else the product followed by the activation kernel
+        (tokenrush/model.py:156-160 with fused.py:67-87)."""
+        if self.layout == "gate_up" and x.shape[0] <= MAX_ROWS:
+            return gfx950.mul_silu(x.contiguous(), self.B, self.s)
+        from .fused import silu_mul
+        return silu_mul(self(x))
 
     def partials(self, x: torch.Tensor) -> torch.Tensor:
         """x [T, K] -> [S, T, N] fp32 whose sum over S is the product (S == 1 unless split-K)."""

@@ -11,7 +11,7 @@ pieces of this package:
       y = mixer(u)                            [M, 6144]   STAND-IN (see below)
       h = out.partials(y)                     [S, M, hidden] fp32 (model.py:85, split-K partials)
       x, n = add_rmsnorm(x, h, ln2)
-      a = silu_mul(gate_up(n))                [M, 17408]  (model.py:156-160)
+      a = silu_mul(gate_up(n))                [M, 17408]  (model.py:156-160), one fused launch
       h = down.partials(a)                    [S, M, hidden] fp32
     _, n = add_rmsnorm(x, h, final_norm); logits = lm_head(n)   [M, 248320]
     greedy accept: n_accepted, tok, pos += n + 1, slot = n (model.py:302-312)
@@ -51,12 +51,12 @@ class StepConfig:
 SMALL = StepConfig(n_layers=4, hidden=512, mlp=1024, gdn_in=2048, attn_qkv=1792, mixer_out=768, vocab=4096)
 
 
-def _random_linear(N, K, gen, device, split_k=1, scale_dtype=torch.bfloat16):
+def _random_linear(N, K, gen, device, split_k=1, scale_dtype=torch.bfloat16, layout="rows"):
     """Codes uniform in 0..15, scale ~U(0.002, 0.02), min ~U(-0.15, -0.01)."""
     q = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=device, generator=gen)
     s = (torch.rand(N, K // 128, device=device, generator=gen) * 0.018 + 0.002).to(scale_dtype)
     m = (torch.rand(N, K // 128, device=device, generator=gen) * 0.14 - 0.15).to(scale_dtype)
-    lin = QLinear(q, s, m, split_k=split_k)
+    lin = QLinear(q, s, m, split_k=split_k, layout=layout)
     del q, s, m
     return lin
 
@@ -68,7 +68,7 @@ class Layer:
         n_in = cfg.attn_qkv if self.attention else cfg.gdn_in
         self.proj = _random_linear(n_in, H, gen, device)
         self.out = _random_linear(H, cfg.mixer_out, gen, device, split_k=4)      # weights.py:163-174
-        self.gate_up = _random_linear(2 * cfg.mlp, H, gen, device)
+        self.gate_up = _random_linear(2 * cfg.mlp, H, gen, device, layout="gate_up")   # silu fused in its epilogue
         self.down = _random_linear(H, cfg.mlp, gen, device, split_k=4)
         self.ln1 = (torch.randn(H, device=device, generator=gen) * 0.1).to(torch.bfloat16)
         self.ln2 = (torch.randn(H, device=device, generator=gen) * 0.1).to(torch.bfloat16)
@@ -107,7 +107,7 @@ class VerifyModel:
             y = self.mixer(L.proj(n))
             h = L.out.partials(y)
             x, n = add_rmsnorm(x, h, L.ln2, cfg.eps)
-            h = L.down.partials(silu_mul(L.gate_up(n)))
+            h = L.down.partials(L.gate_up.silu_mul(n))
         _, n = add_rmsnorm(x, h, self.final_norm, cfg.eps)
         return self.lm_head(n)
 
