@@ -144,6 +144,21 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
                        const float* u, void* ws, size_t ws_bytes, int64_t* n_accepted, int64_t* tok,
                        int64_t* pos, int64_t* slot, int64_t* tokens, int64_t* commit, void* stream);
 
+/* lm_head GEMM with the greedy accept fused into its epilogue (one launch): x [M, K] bf16 hidden
+ * rows, packed [V, K] weight (quad layout; the plan must use one K slot: K <= 6144 for M <= 16,
+ * K <= 3072 above -- otherwise TR_ERR_CONFIG), logits bf16 [M, V] written only when non-null. Each workgroup keeps
+ * the per-row (value, first index) maximum of its bf16 outputs; the last workgroup reduces them
+ * into pred [M] and, when spec_toks is non-null, finishes exactly as tr_accept_greedy does.
+ * workspace: tr_lm_head_workspace_bytes(V, K, M) bytes, zero-filled before first use (every call
+ * leaves its counter at zero); calls that overlap on one device must not share it.
+ * Replaces: lm_head(n) then sample() with temperature 0 (tokenrush/model.py:260, 299-312,
+ * sample.py:37-38), without writing or re-reading the [M, V] logits. */
+size_t tr_lm_head_workspace_bytes(int V, int K, int M);
+int tr_lm_head_greedy(const void* x, const void* packed, void* logits, void* workspace, size_t workspace_bytes,
+                      int M, int V, int K, int group, int scale_dtype, const int64_t* spec_toks, int64_t* pred,
+                      int64_t* n_accepted, int64_t* tok, int64_t* pos, int64_t* slot, int64_t* tokens,
+                      int64_t* commit, void* stream);
+
 /* Draft-tree verify: node 0 is the root (parent -1), parent[i] < i; node i accepted when
  * node_toks[i] == argmax(row parent[i]) and its parent is accepted; the deepest accepted node
  * (lowest index among equals) ends the path. slot = that node, commit = path node indices.

@@ -265,3 +265,39 @@ def test_accept_in_graph_replays(dev):
         check_state(st, ref, M)
         pos = ref["pos"]
         _ = torch.randn(1000, device=dev).sum()                     # eager work between replays
+
+
+@pytest.mark.parametrize("V,M", [(248320, 8), (4096, 1), (4096, 16), (40960, 24)])
+def test_lm_head_greedy_fused(dev, V, M):
+    """lm_head + greedy accept in one launch == lm_head then tr_accept_greedy, bit for bit, and
+    pred == the oracle's argmax of the same logits (M = 24 takes the two-launch path)."""
+    from tokenrush_amd.accept import AcceptState, accept_greedy, lm_head_greedy
+    from tokenrush_amd.quant import QLinear
+    print(f"lm_head_greedy V={V} M={M}", flush=True)
+    K = 5120
+    g = torch.Generator(device="cuda:0").manual_seed(V + M)
+    q = torch.randint(0, 256, (V, K // 2), dtype=torch.uint8, device="cuda:0", generator=g)
+    s = (torch.rand(V, K // 128, device="cuda:0", generator=g) * 0.018 + 0.002).to(torch.bfloat16)
+    m = (torch.rand(V, K // 128, device="cuda:0", generator=g) * 0.14 - 0.15).to(torch.bfloat16)
+    lin = QLinear(q, s, m)
+    del q
+    h = torch.randn(M, K, device="cuda:0", generator=g).to(torch.bfloat16)
+    ref_logits = lin(h)
+    pred = ref_logits.float().argmax(-1)
+    spec = torch.randint(0, V, (M,), device="cuda:0", generator=g)
+    spec[1:min(M, 4)] = pred[:min(M, 4) - 1]                        # a planted accepted prefix
+    st_ref, st = AcceptState(M, "cuda:0"), AcceptState(M, "cuda:0")
+    st_ref.pos.fill_(50)
+    st.pos.fill_(50)
+    accept_greedy(ref_logits, spec, st_ref)
+    logits = lm_head_greedy(lin, h, spec, st, keep_logits=True)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, ref_logits)
+    for name in ("pred", "n_accepted", "tok", "pos", "slot", "tokens", "commit"):
+        assert torch.equal(getattr(st, name), getattr(st_ref, name)), name
+    lg = ref_logits.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(st.pred.cpu().numpy(), oa.argmax_rows(oa.logits_f32(lg)))
+    st2 = AcceptState(M, "cuda:0")
+    assert lm_head_greedy(lin, h, None, st2) is None                 # argmax only, no logits written
+    torch.cuda.synchronize()
+    assert torch.equal(st2.pred, st.pred)

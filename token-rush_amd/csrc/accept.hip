@@ -18,7 +18,7 @@
 //   * ties: argmax takes the first index; the top-64 candidates are ordered by value
 //     descending, then index ascending.
 // Logits are bf16; NaN logits are not supported.
-#include "tr_common.h"
+#include "accept_common.h"
 
 namespace tr {
 
@@ -29,31 +29,6 @@ constexpr int kTopChunk = 4096;    // elements per workgroup in the argmax / top
 constexpr int kRun = 16, kChunk = 1024;
 constexpr int kMaxChunks = 256;    // 1024-element chunks per row: V <= 262144
 constexpr int kCntStride = 64;     // ints between workspace counters (one 256-byte line each)
-
-template <typename T>
-__device__ __forceinline__ void ws_st(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename T>
-__device__ __forceinline__ T ws_ld(const T* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// True (in every thread) for the workgroup that completes `total` arrivals at *cnt; that
-// workgroup also resets the counter. Agent-scope stores made before the call are visible to
-// the last arriver's agent-scope loads.
-__device__ __forceinline__ bool arrive_last(int* cnt, int total) {
-  __shared__ int flag;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flag = old == total - 1;
-    if (flag) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  return flag;
-}
 
 // All threads of the block copy n workspace values into LDS with independent agent-scope loads
 // (a serial chain of such loads would cost a memory round trip each).
@@ -68,24 +43,6 @@ __device__ __forceinline__ float seq_sum(const float* v, int n) {
   float s = 0.f;
   for (int i = 0; i < n; ++i) s = __fadd_rn(s, v[i]);
   return s;
-}
-
-// bf16 bits -> unsigned key increasing with the value.
-__device__ __forceinline__ uint32_t ord16(uint32_t b) { return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u); }
-__device__ __forceinline__ uint32_t unord16(uint32_t k) { return (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu); }
-// (value, index) -> one 64-bit key: larger value first, then smaller index.
-__device__ __forceinline__ uint64_t vkey(uint32_t k16, uint32_t idx) {
-  return ((uint64_t)k16 << 32) | (uint64_t)(0xFFFFFFFFu - idx);
-}
-__device__ __forceinline__ uint32_t vkey_idx(uint64_t k) { return 0xFFFFFFFFu - (uint32_t)k; }
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t w = __shfl_xor(v, o);
-    v = w > v ? w : v;
-  }
-  return v;
 }
 
 // Block-wide exclusive prefix sum of one int per thread (blockDim.x <= 1024), plus the total.
@@ -224,70 +181,6 @@ __device__ void select_top64(const uint32_t (&k16)[E], const uint32_t (&idx)[E],
 }
 
 // ------------------------------------------------------------------ accept outputs
-
-struct AcceptOut {
-  int64_t* pred;        // [M] target token per row (may be null)
-  int64_t* n_accepted;  // [1]
-  int64_t* tok;         // [1] token after the accepted drafts (correction or bonus)
-  int64_t* pos;         // [1] device position, advanced by n + 1
-  int64_t* slot;        // [1] recurrent-state slot to keep (n for chains, best node for trees)
-  int64_t* tokens;      // [M] accepted drafts then tok; -1 beyond
-  int64_t* commit;      // [M] chains: positions pos..pos+n; trees: node indices root..best; -1 beyond
-};
-
-// Engine._verify_step (tokenrush/model.py:302-312): match = pred[:K] == spec[1:M],
-// n = leading matches, tok = pred[n], pos += n + 1, slot = n.
-__device__ void finish_chain(const int64_t* pred, const int64_t* spec, int M, const AcceptOut& o) {
-  int n = 0;
-  while (n < M - 1 && pred[n] == spec[n + 1]) ++n;
-  const int64_t base = *o.pos;
-  const int64_t t = pred[n];
-  *o.n_accepted = n;
-  *o.tok = t;
-  *o.pos = base + n + 1;
-  *o.slot = n;
-  for (int i = 0; i < M; ++i) {
-    o.tokens[i] = i < n ? spec[i + 1] : (i == n ? t : -1);
-    o.commit[i] = i <= n ? base + i : -1;
-  }
-}
-
-// Longest accepted root path of a draft tree (bench/tree_accept.py:91-100): node 0 is the
-// root; node i > 0 (parent[i] < i) is accepted when its token equals the prediction of its
-// parent's row and the parent is accepted. Deepest accepted node wins, lowest index on ties.
-// Runs on one thread with its node arrays in LDS (no scratch, no registers held by the
-// chunk-scanning part of the kernel).
-__device__ void finish_tree(const int64_t* pred, const int64_t* node_tok, const int32_t* parent, int M,
-                                         const AcceptOut& o) {
-  __shared__ int ok[32], depth[32], path[32];
-  ok[0] = 1;
-  depth[0] = 0;
-  int best = 0;
-  for (int i = 1; i < M; ++i) {
-    const int p = parent[i];
-    const bool valid = p >= 0 && p < i;  // a malformed parent array accepts nothing below it
-    depth[i] = valid ? depth[p] + 1 : 0;
-    ok[i] = valid && ok[p] && node_tok[i] == pred[p];
-    if (ok[i] && depth[i] > depth[best]) best = i;
-  }
-  const int n = depth[best];
-  for (int j = best, d = n; d >= 0; --d) {
-    path[d] = j;
-    j = d > 0 ? parent[j] : 0;
-  }
-  const int64_t base = *o.pos;
-  const int64_t t = pred[best];
-  *o.n_accepted = n;
-  *o.tok = t;
-  *o.pos = base + n + 1;
-  *o.slot = best;
-  for (int i = 0; i < M; ++i) {
-    o.tokens[i] = i < n ? node_tok[path[i + 1]] : (i == n ? t : -1);
-    o.commit[i] = i <= n ? path[i] : -1;
-  }
-}
-
-// ------------------------------------------------------------------ argmax kernel (greedy, tree)
 
 enum { FIN_NONE = 0, FIN_CHAIN = 1, FIN_TREE = 2 };
 

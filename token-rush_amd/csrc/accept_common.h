@@ -1,0 +1,116 @@
+// Device helpers shared by the accept kernels (accept.hip) and the GEMM's fused argmax epilogue
+// (int4_gemm.hip): agent-scope workspace access, the last-arriver counter, ordered (value, index)
+// keys and the verify-step finishes (tokenrush/model.py:302-312, bench/tree_accept.py:91-100).
+#pragma once
+#include "tr_common.h"
+
+namespace tr {
+
+template <typename T>
+__device__ __forceinline__ void ws_st(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T ws_ld(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// True (in every thread) for the workgroup that completes `total` arrivals at *cnt; that
+// workgroup also resets the counter. Agent-scope stores made before the call are visible to
+// the last arriver's agent-scope loads.
+__device__ __forceinline__ bool arrive_last(int* cnt, int total) {
+  __shared__ int flag;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flag = old == total - 1;
+    if (flag) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  return flag;
+}
+
+// bf16 bits -> unsigned key increasing with the value.
+__device__ __forceinline__ uint32_t ord16(uint32_t b) { return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u); }
+__device__ __forceinline__ uint32_t unord16(uint32_t k) { return (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu); }
+// (value, index) -> one 64-bit key: larger value first, then smaller index.
+__device__ __forceinline__ uint64_t vkey(uint32_t k16, uint32_t idx) {
+  return ((uint64_t)k16 << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+__device__ __forceinline__ uint32_t vkey_idx(uint64_t k) { return 0xFFFFFFFFu - (uint32_t)k; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t w = __shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+struct AcceptOut {
+  int64_t* pred;        // [M] target token per row (may be null)
+  int64_t* n_accepted;  // [1]
+  int64_t* tok;         // [1] token after the accepted drafts (correction or bonus)
+  int64_t* pos;         // [1] device position, advanced by n + 1
+  int64_t* slot;        // [1] recurrent-state slot to keep (n for chains, best node for trees)
+  int64_t* tokens;      // [M] accepted drafts then tok; -1 beyond
+  int64_t* commit;      // [M] chains: positions pos..pos+n; trees: node indices root..best; -1 beyond
+};
+
+// Engine._verify_step (tokenrush/model.py:302-312): match = pred[:K] == spec[1:M],
+// n = leading matches, tok = pred[n], pos += n + 1, slot = n.
+static __device__ void finish_chain(const int64_t* pred, const int64_t* spec, int M, const AcceptOut& o) {
+  int n = 0;
+  while (n < M - 1 && pred[n] == spec[n + 1]) ++n;
+  const int64_t base = *o.pos;
+  const int64_t t = pred[n];
+  *o.n_accepted = n;
+  *o.tok = t;
+  *o.pos = base + n + 1;
+  *o.slot = n;
+  for (int i = 0; i < M; ++i) {
+    o.tokens[i] = i < n ? spec[i + 1] : (i == n ? t : -1);
+    o.commit[i] = i <= n ? base + i : -1;
+  }
+}
+
+// Longest accepted root path of a draft tree (bench/tree_accept.py:91-100): node 0 is the
+// root; node i > 0 (parent[i] < i) is accepted when its token equals the prediction of its
+// parent's row and the parent is accepted. Deepest accepted node wins, lowest index on ties.
+// Runs on one thread with its node arrays in LDS (no scratch, no registers held by the
+// chunk-scanning part of the kernel).
+static __device__ void finish_tree(const int64_t* pred, const int64_t* node_tok, const int32_t* parent, int M,
+                                         const AcceptOut& o) {
+  __shared__ int ok[32], depth[32], path[32];
+  ok[0] = 1;
+  depth[0] = 0;
+  int best = 0;
+  for (int i = 1; i < M; ++i) {
+    const int p = parent[i];
+    const bool valid = p >= 0 && p < i;  // a malformed parent array accepts nothing below it
+    depth[i] = valid ? depth[p] + 1 : 0;
+    ok[i] = valid && ok[p] && node_tok[i] == pred[p];
+    if (ok[i] && depth[i] > depth[best]) best = i;
+  }
+  const int n = depth[best];
+  for (int j = best, d = n; d >= 0; --d) {
+    path[d] = j;
+    j = d > 0 ? parent[j] : 0;
+  }
+  const int64_t base = *o.pos;
+  const int64_t t = pred[best];
+  *o.n_accepted = n;
+  *o.tok = t;
+  *o.pos = base + n + 1;
+  *o.slot = best;
+  for (int i = 0; i < M; ++i) {
+    o.tokens[i] = i < n ? node_tok[path[i + 1]] : (i == n ? t : -1);
+    o.commit[i] = i <= n ? path[i] : -1;
+  }
+}
+
+// ------------------------------------------------------------------ argmax kernel (greedy, tree)
+
+}  // namespace tr

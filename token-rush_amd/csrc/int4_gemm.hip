@@ -41,7 +41,7 @@
 // (deterministic). With S > 1 slots, slots write fp32 partials: either the caller's
 // [S, M, N] buffer (the contract of the reference's partials(), tokenrush/quant.py:381-391,
 // tokenrush/marlin.py:158-168) or a workspace the last-arriving slot reduces into bf16.
-#include "tr_common.h"
+#include "accept_common.h"
 
 namespace tr {
 
@@ -164,6 +164,13 @@ struct GemmArgs {
   int RB;                 // strips per LDS reduction batch
   int mode;
   int silu;               // 1: gate/up pair layout, out = silu(gate) * up, bf16 [M, N / 2]
+  // Fused argmax (S == 1): per-row (value, first index) max of the bf16 outputs; the last
+  // workgroup reduces the per-workgroup keys and finishes the greedy accept when spec != null.
+  int argmax;
+  uint64_t* am_keys;      // [grid, M] workspace
+  int* am_cnt;            // arrival counter, zero between calls
+  const int64_t* spec;    // [M] committed token + drafts, or null (argmax only)
+  AcceptOut o;            // o.pred [M] always; the rest when spec != null
 };
 
 // One accumulator tile element: (mt, lane, r) -> output row m = 16 mt + 4 (lane / 16) + r,
@@ -171,6 +178,8 @@ struct GemmArgs {
 template <int MT, int GW, bool F16S>
 __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   extern __shared__ float red[];  // [2][RB][W][MT][64][4]
+  __shared__ uint64_t rowbest[32];  // fused argmax: best key per output row
+  if (threadIdx.x < 32) rowbest[threadIdx.x] = 0;
   const int G = a.K / kGroup;
   const int Gp = padded_groups(a.K);
   const int nstrips = a.N / 16;
@@ -311,8 +320,12 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
               const int m = rem >> 4, n16 = rem & 15;
               const float v = wave_sum(sidx, m, n16);
               const int n = 16 * phys(r_first + sidx) + n16;
-              if (a.mode == OUT_BF16)
-                ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v);
+              if (a.mode == OUT_BF16) {
+                const uint32_t b = f32_to_bf16_bits(v);
+                if (a.out) ((uint16_t*)a.out)[(size_t)m * a.N + n] = (uint16_t)b;
+                if (a.argmax) __hip_atomic_fetch_max(&rowbest[m], vkey(ord16(b), n), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+              }
               else if (a.mode == OUT_PARTIAL)
                 ((float*)a.out)[((size_t)slot * a.M + m) * a.N + n] = v;
               else  // agent-scope store: written through to the coherence point, no L2 flush needed
@@ -329,6 +342,31 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     }
   }
 
+  if (a.argmax) {
+    // Publish this workgroup's row keys; the last workgroup reduces them (fixed order is not
+    // needed: a max of unique keys) and finishes the accept.
+    __syncthreads();
+    if (threadIdx.x < a.M) ws_st(a.am_keys + (size_t)blockIdx.x * a.M + threadIdx.x, rowbest[threadIdx.x]);
+    if (!arrive_last(a.am_cnt, gridDim.x)) return;
+    __shared__ int64_t pred[32], spec[32];
+    const int nwv = blockDim.x >> 6;
+    for (int m = threadIdx.x >> 6; m < a.M; m += nwv) {
+      uint64_t best = 0;
+      for (int g = lane; g < (int)gridDim.x; g += 64) {
+        const uint64_t k = ws_ld(a.am_keys + (size_t)g * a.M + m);
+        best = k > best ? k : best;
+      }
+      best = wave_max_u64(best);
+      if (lane == 0) {
+        pred[m] = vkey_idx(best);
+        a.o.pred[m] = pred[m];
+      }
+    }
+    if (a.spec && threadIdx.x < a.M) spec[threadIdx.x] = a.spec[threadIdx.x];
+    __syncthreads();
+    if (a.spec && threadIdx.x == 0) finish_chain(pred, spec, a.M, a.o);
+    return;
+  }
   if (a.mode != OUT_BF16_VIA_WS) return;
   // Last-arriving slot of this row range sums the S partials in slot order -> bf16. The
   // partials were stored at agent scope; waiting for those stores to complete before the
@@ -585,15 +623,20 @@ size_t tr_gemm_workspace_bytes(int N, int K, int M) {
   return ws_counter_bytes() + (size_t)p.S * M * N * sizeof(float);
 }
 
+struct ArgmaxOut {
+  const int64_t* spec;
+  AcceptOut o;
+};
+
 static int gemm_impl(const void* x, const void* packed, void* out, void* partials, void* workspace,
                      size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots, int R,
-                     int silu, void* stream) {
+                     int silu, void* stream, const ArgmaxOut* am = nullptr) {
   if (group != kGroup) return TR_ERR_CONFIG;
   if (M < 0 || M > 32 || !shape_ok(N, K)) return TR_ERR_SHAPE;
   if (silu && partials) return TR_ERR_ARG;
   if (silu && N % 32) return TR_ERR_SHAPE;
   if (M == 0) return TR_OK;
-  if (!x || !packed || (!out == !partials)) return TR_ERR_ARG;
+  if (!x || !packed || (am ? partials != nullptr : (!out == !partials))) return TR_ERR_ARG;
   if (scale_dtype != 0 && scale_dtype != 1) return TR_ERR_ARG;
   Plan p;
   if (!make_plan(N, K, M, n_slots, R, &p)) return TR_ERR_CONFIG;
@@ -609,6 +652,25 @@ static int gemm_impl(const void* x, const void* packed, void* out, void* partial
   a.ws_part = nullptr;
   a.ws_cnt = nullptr;
   a.silu = silu;
+  a.argmax = 0;
+  a.am_keys = nullptr;
+  a.am_cnt = nullptr;
+  a.spec = nullptr;
+  a.o = AcceptOut{};
+  if (am) {
+    // fused argmax: one K slot (the per-row keys come from complete outputs), keys after the
+    // counter line of the workspace
+    if (p.S != 1 || partials || silu) return TR_ERR_CONFIG;
+    const size_t need = kWsCounterStride * sizeof(int) + (size_t)p.grid_n * M * sizeof(uint64_t);
+    if (!workspace || workspace_bytes < need || !am->o.pred) return TR_ERR_ARG;
+    if (am->spec && (!am->o.n_accepted || !am->o.tok || !am->o.pos || !am->o.slot || !am->o.tokens || !am->o.commit))
+      return TR_ERR_ARG;
+    a.argmax = 1;
+    a.am_cnt = (int*)workspace;
+    a.am_keys = (uint64_t*)((char*)workspace + kWsCounterStride * sizeof(int));
+    a.spec = am->spec;
+    a.o = am->o;
+  }
   if (partials) {
     a.mode = OUT_PARTIAL;
     a.out = partials;
@@ -637,6 +699,22 @@ int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials
 int tr_int4_gemm_silu(const void* x, const void* packed, void* out, void* workspace, size_t workspace_bytes, int M,
                       int N, int K, int group, int scale_dtype, void* stream) {
   return gemm_impl(x, packed, out, nullptr, workspace, workspace_bytes, M, N, K, group, scale_dtype, 0, 0, 1, stream);
+}
+
+size_t tr_lm_head_workspace_bytes(int N, int K, int M) {
+  Plan p;
+  if (!shape_ok(N, K) || M < 1 || M > 32 || !make_plan(N, K, M, 0, 0, &p) || p.S != 1) return 0;
+  return kWsCounterStride * sizeof(int) + (size_t)p.grid_n * M * sizeof(uint64_t);
+}
+
+int tr_lm_head_greedy(const void* x, const void* packed, void* logits, void* workspace, size_t workspace_bytes,
+                      int M, int N, int K, int group, int scale_dtype, const int64_t* spec_toks, int64_t* pred,
+                      int64_t* n_accepted, int64_t* tok, int64_t* pos, int64_t* slot, int64_t* tokens,
+                      int64_t* commit, void* stream) {
+  if (M < 1) return TR_ERR_SHAPE;
+  ArgmaxOut am{spec_toks, AcceptOut{pred, n_accepted, tok, pos, slot, tokens, commit}};
+  return gemm_impl(x, packed, logits, nullptr, workspace, workspace_bytes, M, N, K, group, scale_dtype, 0, 0, 0, stream,
+                   &am);
 }
 
 int tr_int4_gemm(const void* x, const void* packed, void* out, void* partials, void* workspace,

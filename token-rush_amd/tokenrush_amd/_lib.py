@@ -36,6 +36,8 @@ SIGNATURES = {
     "tr_unpack_int4_pairs": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "tr_dequant_int4": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "tr_accept_workspace_bytes": (_S, [_I, _I]),
+    "tr_lm_head_workspace_bytes": (_S, [_I, _I, _I]),
+    "tr_lm_head_greedy": (_I, [_P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tr_argmax_rows": (_I, [_P, _I, _I, _P, _S, _P, _P]),
     "tr_accept_greedy": (_I, [_P, _I, _I, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tr_accept_tree": (_I, [_P, _I, _I, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _P]),

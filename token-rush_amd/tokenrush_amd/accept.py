@@ -124,3 +124,49 @@ def commit_rows(cache: torch.Tensor, st: AcceptState, max_n: int = 31):
     rc = _lib.lib().tr_commit_rows(_lib.ptr(cache), planes, plane_stride, row_bytes, _lib.ptr(st.pos),
                                    _lib.ptr(st.n_accepted), _lib.ptr(st.commit), max_n, _lib.stream_of(cache))
     _lib.check(rc, "tr_commit_rows")
+
+
+_lm_ws = {}
+
+
+def lm_head_greedy(lm_head, hidden: torch.Tensor, spec_toks: torch.Tensor, st: AcceptState,
+                   keep_logits: bool = False):
+    """logits = lm_head(hidden) and the greedy verify accept in one launch (the GEMM's epilogue
+    keeps each row's argmax; the last workgroup finishes the accept exactly as accept_greedy
+    does). lm_head: a gfx950 QLinear [V, K]; hidden [M, K] bf16. Returns the logits [M, V] when
+    keep_logits (the reference keeps them, model.py:300), else None -- then they are never
+    written. spec_toks None: only st.pred is written (argmax per row). Shapes whose plan splits K
+    across workgroups (M > 16 at K = 5120) run the product and then the accept kernel."""
+    from . import gfx950
+    if lm_head.backend != "gfx950" or lm_head.layout != "rows":
+        raise RuntimeError("lm_head_greedy needs a gfx950 QLinear in the plain row layout")
+    _lib.require_gpu(hidden)
+    M, K = hidden.shape
+    V = lm_head.shape[0]
+    if hidden.dtype != torch.bfloat16 or K != lm_head.shape[1] or st.M < M:
+        raise RuntimeError("lm_head_greedy: hidden must be bf16 [M, K] matching the weight")
+    need = int(_lib.lib().tr_lm_head_workspace_bytes(V, K, M))
+    if need == 0:                  # more than one K slot: the product, then the accept kernel
+        logits = lm_head(hidden)
+        if spec_toks is None:
+            _lib.check(_lib.lib().tr_argmax_rows(_lib.ptr(logits), M, V, _lib.ptr(workspace(M, V, hidden.device)),
+                                                 workspace(M, V, hidden.device).numel(), _lib.ptr(st.pred),
+                                                 _lib.stream_of(logits)), "tr_argmax_rows")
+        else:
+            accept_greedy(logits, spec_toks, st)
+        return logits if keep_logits else None
+    key = hidden.device.index or 0
+    ws = _lm_ws.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=hidden.device)
+        _lm_ws[key] = ws
+    logits = torch.empty(M, V, dtype=torch.bfloat16, device=hidden.device) if keep_logits else None
+    spec = None if spec_toks is None else spec_toks[:M].to(torch.long).contiguous()
+    x = hidden.contiguous()
+    P = _lib.ptr
+    rc = _lib.lib().tr_lm_head_greedy(P(x), P(lm_head.B), P(logits), P(ws), ws.numel(), M, V, K, 128,
+                                      gfx950.SCALE_DTYPES[lm_head.s.dtype], P(spec), P(st.pred), P(st.n_accepted),
+                                      P(st.tok), P(st.pos), P(st.slot), P(st.tokens), P(st.commit),
+                                      _lib.stream_of(x))
+    _lib.check(rc, "tr_lm_head_greedy")
+    return logits

@@ -14,7 +14,8 @@ pieces of this package:
       a = silu_mul(gate_up(n))                [M, 17408]  (model.py:156-160), one fused launch
       h = down.partials(a)                    [S, M, hidden] fp32
     _, n = add_rmsnorm(x, h, final_norm); logits = lm_head(n)   [M, 248320]
-    greedy accept: n_accepted, tok, pos += n + 1, slot = n (model.py:302-312)
+    greedy accept: n_accepted, tok, pos += n + 1, slot = n (model.py:302-312), in the lm_head
+    GEMM's epilogue (one launch)
 
 Stand-ins: the GDN recurrence (fused.py:119-237) and attention (fused.py:247-470) are not part of
 this build; each mixer is replaced by silu(u[:, :6144]) * u[:, 6144:12288], one launch that reads
@@ -27,7 +28,7 @@ from dataclasses import dataclass
 import torch
 
 from . import gfx950
-from .accept import AcceptState, accept_greedy
+from .accept import AcceptState, lm_head_greedy
 from .fused import add_rmsnorm, silu_mul
 from .quant import QLinear
 
@@ -98,8 +99,8 @@ class VerifyModel:
         F = self.cfg.mixer_out
         return silu_mul(u[:, :2 * F])
 
-    def body(self, x0: torch.Tensor) -> torch.Tensor:
-        """x0 [M, hidden] bf16 -> logits [M, vocab] bf16."""
+    def hidden(self, x0: torch.Tensor) -> torch.Tensor:
+        """x0 [M, hidden] bf16 -> post-final-norm hidden [M, hidden] bf16 (model.py:252-254)."""
         cfg = self.cfg
         x, h = x0, None
         for L in self.layers:
@@ -109,13 +110,16 @@ class VerifyModel:
             x, n = add_rmsnorm(x, h, L.ln2, cfg.eps)
             h = L.down.partials(L.gate_up.silu_mul(n))
         _, n = add_rmsnorm(x, h, self.final_norm, cfg.eps)
-        return self.lm_head(n)
+        return n
+
+    def body(self, x0: torch.Tensor) -> torch.Tensor:
+        """x0 [M, hidden] bf16 -> logits [M, vocab] bf16."""
+        return self.lm_head(self.hidden(x0))
 
     def step(self, x0: torch.Tensor, spec_toks: torch.Tensor, st: AcceptState) -> torch.Tensor:
-        """Body + lm_head + greedy accept/commit. Returns the logits (graph-owned under capture)."""
-        logits = self.body(x0)
-        accept_greedy(logits, spec_toks, st)
-        return logits
+        """Body + lm_head with the greedy accept/commit in its epilogue (one launch). Returns the
+        logits, kept as the reference keeps them (model.py:300; graph-owned under capture)."""
+        return lm_head_greedy(self.lm_head, self.hidden(x0), spec_toks, st, keep_logits=True)
 
 
 def prepare(model: VerifyModel, M: int):
