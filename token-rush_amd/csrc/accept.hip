@@ -180,6 +180,53 @@ __device__ void select_top64(const uint32_t (&k16)[E], const uint32_t (&idx)[E],
   __syncthreads();
 }
 
+
+// Wave-wide merge of two descending 64-key lists, one key per lane: lane i keeps the larger of
+// a[i] and b[63 - i] (the top 64 of the union, as a bitonic sequence), then a bitonic merge
+// sorts it descending. Keys are vkey()s: value descending, index ascending.
+__device__ __forceinline__ uint64_t bitonic_sort_desc(uint64_t key, int lane) {
+#pragma unroll
+  for (int stride = 32; stride > 0; stride >>= 1) {
+    const uint64_t other = __shfl_xor(key, stride);
+    const bool lower = (lane & stride) == 0;
+    key = lower ? (other > key ? other : key) : (other < key ? other : key);
+  }
+  return key;
+}
+__device__ __forceinline__ uint64_t merge_top64(uint64_t a, uint64_t b_rev, int lane) {
+  return bitonic_sort_desc(a > b_rev ? a : b_rev, lane);
+}
+
+// Top 64 (descending) of n <= 16 * waves sorted 64-key lists in the workspace (list c at
+// src + 128 c: 64 (value key, index) pairs), merged by the block's waves; result in LDS
+// out_k / out_i.
+__device__ void merge_lists_top64(const uint32_t* src, int n, uint32_t* out_k, uint32_t* out_i) {
+  constexpr int kPerWave = 16;  // lists per wave: n <= 64 with 4 waves
+  __shared__ uint64_t wres[16][kCand];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // every list of this wave is loaded before any merge: independent loads, one round trip
+  uint32_t kv[kPerWave], iv[kPerWave];
+#pragma unroll
+  for (int j = 0; j < kPerWave; ++j) {
+    const int c = wid + j * nw;
+    const uint32_t* l = src + (size_t)c * kCand * 2 + 2 * (kCand - 1 - lane);  // reversed: ascending
+    kv[j] = c < n ? ws_ld(l) : 0u;
+    iv[j] = c < n ? ws_ld(l + 1) : 0xFFFFFFFFu;
+  }
+  uint64_t acc = bitonic_sort_desc(vkey(kv[0], iv[0]), lane);
+#pragma unroll
+  for (int j = 1; j < kPerWave; ++j)
+    if (wid + j * nw < n) acc = merge_top64(acc, vkey(kv[j], iv[j]), lane);
+  wres[wid][lane] = acc;
+  __syncthreads();
+  if (wid == 0) {
+    for (int w = 1; w < nw; ++w) acc = merge_top64(acc, wres[w][kCand - 1 - lane], lane);
+    out_k[lane] = (uint32_t)(acc >> 32);
+    out_i[lane] = vkey_idx(acc);
+  }
+  __syncthreads();
+}
+
 // ------------------------------------------------------------------ accept outputs
 
 enum { FIN_NONE = 0, FIN_CHAIN = 1, FIN_TREE = 2 };
@@ -360,20 +407,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     ws_st(mine + 2 * threadIdx.x + 1, ti[threadIdx.x]);
   }
   if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
-  // merge: the nch sorted lists in chunk order keep equal values in index order
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int c = threadIdx.x * E + e;  // candidate number = chunk * 64 + rank
-    if (c < a.nch * kCand) {
-      const uint32_t* src = a.cand + (size_t)row * a.nch * kCand * 2 + 2 * c;
-      k16[e] = ws_ld(src);
-      idx[e] = ws_ld(src + 1);
-    } else {
-      k16[e] = 0;
-      idx[e] = 0xFFFFFFFFu;
-    }
-  }
-  select_top64<E>(k16, idx, tk, ti);
+  merge_lists_top64(a.cand + (size_t)row * a.nch * kCand * 2, a.nch, tk, ti);
   if (threadIdx.x < 64) {
     const int64_t t = sample_pick(tk, ti, *a.temperature, *a.top_p, *a.top_k, a.u[row]);
     if (threadIdx.x == 0) {
