@@ -190,6 +190,27 @@ int tr_add_rmsnorm(const void* x, const void* h, int h_mode, int n_slots, const 
  * Replaces: silu_mul (tokenrush/fused.py:67-87). */
 int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* stream);
 
+/* ---------------------------------------------------------------- GDN (gated delta rule) step */
+
+/* Bytes of the workspace tr_gdn_step needs for M tokens and HV value heads (0 if unsupported).
+ * Zero-filled once by the caller; every call leaves its counters at zero. */
+size_t tr_gdn_workspace_bytes(int M, int HV);
+
+/* One M-token (1..8) GDN step of one layer: causal conv (kernel 4) over the ring with silu, b/a gates
+ * from x . ba_w, L2-normalised q and k, the gated delta rule with the state after token t written to
+ * rec slot t, and the gated RMSNorm -> y.
+ *   qkvz [M, ld] bf16 (q | k | v | z, ld >= 2 H K + 2 HV V), x [M, hidden] bf16, ba_w [2 HV, hidden]
+ *   bf16, ring [2 H K + HV V, R] bf16 (columns (pos + t) % R updated), conv_w [2 H K + HV V, 4] bf16,
+ *   A and dt_bias [HV] fp32, rec fp32 slots slot_stride floats apart, each [HV, K, V]; the committed
+ *   state is slot *slot (device int64); pos: device int64 position of token 0; norm_w [V] bf16;
+ *   y [M, HV V] bf16. K == V == 128, HV % H == 0, R >= M + 3, hidden % 8 == 0.
+ * Replaces: gdn_step_fused (tokenrush/fused.py:119-236: _gdn_step_fused_kernel + _gated_norm_kernel),
+ * the fused path of gdn_forward (tokenrush/model.py:76-80). */
+int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void* ring, const void* conv_w,
+                const float* A, const float* dt_bias, float* rec, long slot_stride, const int64_t* slot,
+                const void* norm_w, const int64_t* pos, void* y, void* workspace, size_t workspace_bytes, int M,
+                int H, int HV, int K, int V, int hidden, int R, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
