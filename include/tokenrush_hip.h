@@ -211,6 +211,29 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
                 const void* norm_w, const int64_t* pos, void* y, void* workspace, size_t workspace_bytes, int M,
                 int H, int HV, int K, int V, int hidden, int R, float eps, void* stream);
 
+/* ---------------------------------------------------------------- attention over an FP8 KV cache */
+
+/* Bytes of the split-partials workspace of tr_attn_decode (0 if unsupported). */
+size_t tr_attn_workspace_bytes(int M, int HQ, int nsplit);
+
+/* Prep of M (1..8) new tokens of one attention layer: q and k RMSNorm with (1 + w) gain, partial
+ * rope on the first rotary_dim dims (a power of two) at positions *pos + t, q_out [M, HQ, D] bf16,
+ * and cache rows *pos + t of k_cache / v_cache ([HKV, maxlen, D] float8_e4m3fn) with their scales
+ * k_scale / v_scale ([HKV, maxlen] fp32, amax / 448). qkv [M, ld] bf16 = [HQ (q | gate) 2D | HKV D |
+ * HKV D]; cos / sin [max_pos, rotary_dim] bf16. D == 256.
+ * Replaces: attn_prep (tokenrush/fused.py:247-325). */
+int tr_attn_prep(const void* qkv, int ld, const void* q_norm_w, const void* k_norm_w, const void* cos,
+                 const void* sin, int rotary_dim, const int64_t* pos, void* k_cache, void* v_cache, float* k_scale,
+                 float* v_scale, int maxlen, void* q_out, int M, int HQ, int HKV, int D, float eps, void* stream);
+
+/* Flash-decoding of M (1..8) query tokens over cache rows 0..*pos + M - 1 (query t sees rows
+ * <= *pos + t): nsplit key-range splits (two launches: split, then combine + sigmoid output gate
+ * from qkv) -> out [M, HQ D] bf16. (HQ / HKV) * M <= 64, D == 256.
+ * Replaces: attn_decode_fused (tokenrush/fused.py:355-470: _attn_split_kernel + _attn_reduce_kernel). */
+int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, const void* v_cache,
+                   const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos, void* out,
+                   void* workspace, size_t workspace_bytes, int M, int HQ, int HKV, int D, int nsplit, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

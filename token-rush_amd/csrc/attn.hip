@@ -1,0 +1,459 @@
+// Full-attention verify step for gfx950 over an FP8 (e4m3fn) KV cache with per-(head, position)
+// fp32 scales: the prep of the M new tokens (q/k RMSNorm, partial rope, cache write) and
+// flash-decoding (split over the live keys, then a reduce with the sigmoid output gate).
+//
+// Follows the reference's Triton kernels (tokenrush/fused.py:247-325 _attn_prep_kernel and
+// attn_prep, :355-470 _attn_split_kernel, _attn_reduce_kernel and attn_decode_fused):
+//   prep (heads 0..HQ-1 from the q part of qkv [HQ (q | gate) 2D | HKV D | HKV D], heads HQ..
+//   for k): xn = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)); on the first RD dims, with halves
+//   x1, x2 and the position's cos/sin: o1 = bf16(bf16(x1 c) + bf16(-x2 s)),
+//   o2 = bf16(bf16(x2 c) + bf16(x1 s)). q is written bf16; k and the raw v go to cache row
+//   pos + t as fp8(x / sc) with sc = max(amax(x), 1e-6) / 448.
+//   attention: query t of head h sees cache rows <= pos + t; scores q . bf16(k8 * ksc) / sqrt(D);
+//   online softmax in fp32 with l summed before the value scale, P = bf16(p * vsc), acc += P v8;
+//   splits combined by their maxima; o = bf16(acc / l) * bf16(sigmoid(gate)), bf16 out.
+//
+// MI355X layout of the split kernel: one workgroup of four waves per (kv head, split); the
+// G * M query rows of the kv head (G = HQ / HKV query heads per token) are 16-row MFMA tiles,
+// one per wave. Keys stream through LDS 32 at a time: K dequantized to bf16 row-major, V
+// converted to bf16 and transposed (d-major) while it is written. Scores are computed transposed,
+// S^T = K Q^T (v_mfma_f32_16x16x32_bf16, Q^T stationary in registers), which leaves each lane
+// the scores of one query row for 8 keys: exactly the B operand of O^T = V^T P^T once the key
+// order inside the 32-key step is permuted the same way on the V^T side. Row maxima and sums
+// need two xor shuffles. Each wave keeps O^T for its 16 rows x 256 d in 64 registers.
+#include "accept_common.h"
+
+namespace tr {
+
+constexpr int kAttnD = 256;      // head dim
+constexpr int kAttnBlk = 32;     // keys per LDS block
+constexpr int kAttnMaxM = 8;     // query tokens per step
+constexpr int kAttnWaves = 4;
+constexpr int kKPitch = kAttnD + 8;     // bf16 elements per K row in LDS
+constexpr int kVPitch = kAttnBlk + 4;   // bf16 elements per V^T row (one d) in LDS
+constexpr float kFp8Max = 448.f;
+
+// ------------------------------------------------------------------ fp8 e4m3fn (OCP) helpers
+
+// fp8 e4m3fn bits -> fp32 (exact). NaN (0x7F / 0xFF) is never produced by this path's writers.
+__device__ __forceinline__ float fp8_to_f32(uint32_t b) {
+  const uint32_t e = (b >> 3) & 0xF, m = b & 7;
+  const float mag = e == 0 ? (float)m * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (b & 0x80) ? -mag : mag;
+}
+
+// fp32 -> fp8 e4m3fn bits, round to nearest even; magnitudes past the largest finite value
+// (448) saturate to it (the writers keep |x| <= 448 up to rounding).
+__device__ __forceinline__ uint32_t f32_to_fp8(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80;
+  const float a = fabsf(x);
+  uint32_t code;
+  if (a < 0x1p-6f) {
+    code = (uint32_t)__builtin_rintf(a * 512.f);  // subnormal steps of 2^-9; 8 becomes 2^-6
+  } else {
+    uint32_t v = __float_as_uint(a);
+    v += 0x7FFFFu + ((v >> 20) & 1u);            // round the mantissa to 3 bits
+    const int e = (int)(v >> 23) - 120;
+    const uint32_t m = (v >> 20) & 7;
+    code = (e > 15 || (e == 15 && m == 7)) ? 0x7Eu : ((uint32_t)e << 3) | m;
+  }
+  return sign | code;
+}
+
+__device__ __forceinline__ float bf16r_a(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+// ------------------------------------------------------------------ prep
+
+struct AttnPrepArgs {
+  const uint16_t* qkv;   // [M, QKV] bf16
+  const uint16_t* qn_w;  // [D] bf16
+  const uint16_t* kn_w;  // [D] bf16
+  const uint16_t* cos;   // [max_pos, RD] bf16
+  const uint16_t* sin;
+  const int64_t* pos;
+  uint8_t* k_cache;      // [HKV, maxlen, D] fp8
+  uint8_t* v_cache;
+  float* k_scale;        // [HKV, maxlen]
+  float* v_scale;
+  uint16_t* q_out;       // [M, HQ, D] bf16
+  int HQ, HKV, RD, maxlen, ld;
+  float eps;
+};
+
+// One wave per (head, token); lane l holds dims 4 l .. 4 l + 3.
+__global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
+  const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  const int64_t p = *a.pos + t;
+  const bool isq = head < a.HQ;
+  const int j = head - a.HQ;
+  const uint16_t* row = a.qkv + (size_t)t * a.ld;
+  const uint16_t* src = isq ? row + (size_t)head * 2 * kAttnD : row + (size_t)a.HQ * 2 * kAttnD + (size_t)j * kAttnD;
+  const uint16_t* w = isq ? a.qn_w : a.kn_w;
+  const int d0 = 4 * lane;
+  float x[4], wv[4];
+  {
+    const uint2 xu = *(const uint2*)(src + d0), wu = *(const uint2*)(w + d0);
+    x[0] = bf16_bits_to_f32(xu.x & 0xFFFFu);
+    x[1] = bf16_bits_to_f32(xu.x >> 16);
+    x[2] = bf16_bits_to_f32(xu.y & 0xFFFFu);
+    x[3] = bf16_bits_to_f32(xu.y >> 16);
+    wv[0] = bf16_bits_to_f32(wu.x & 0xFFFFu);
+    wv[1] = bf16_bits_to_f32(wu.x >> 16);
+    wv[2] = bf16_bits_to_f32(wu.y & 0xFFFFu);
+    wv[3] = bf16_bits_to_f32(wu.y >> 16);
+  }
+  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const float inv = 1.f / sqrtf(ss / (float)kAttnD + a.eps);
+  float xn[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xn[i] = bf16r_a(x[i] * inv * (1.f + wv[i]));
+  // partial rope on dims < RD: dim r pairs with r + RD / 2 (a lane RD / 8 lanes away)
+  const int half = a.RD / 2;
+  float out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float other = __shfl_xor(xn[i], half / 4);
+    const int d = d0 + i;
+    out[i] = xn[i];
+    if (d < a.RD) {
+      const int r = d < half ? d : d - half;
+      const float c = bf16_bits_to_f32(a.cos[(size_t)p * a.RD + r]);
+      const float s = bf16_bits_to_f32(a.sin[(size_t)p * a.RD + r]);
+      out[i] = d < half ? bf16r_a(bf16r_a(xn[i] * c) + bf16r_a(-other * s))
+                        : bf16r_a(bf16r_a(xn[i] * c) + bf16r_a(other * s));
+    }
+  }
+  if (isq) {
+    uint16_t* qo = a.q_out + ((size_t)t * a.HQ + head) * kAttnD + d0;
+    uint2 st;
+    st.x = (uint32_t)f32_to_bf16_bits(out[0]) | ((uint32_t)f32_to_bf16_bits(out[1]) << 16);
+    st.y = (uint32_t)f32_to_bf16_bits(out[2]) | ((uint32_t)f32_to_bf16_bits(out[3]) << 16);
+    *(uint2*)qo = st;
+    return;
+  }
+  // key: fp8 with one scale per (head, position)
+  float am = fmaxf(fmaxf(fabsf(out[0]), fabsf(out[1])), fmaxf(fabsf(out[2]), fabsf(out[3])));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+  const float sc = fmaxf(am, 1e-6f) / kFp8Max;
+  const size_t crow = ((size_t)j * a.maxlen + p);
+  uint32_t kb = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kb |= f32_to_fp8(out[i] / sc) << (8 * i);
+  *(uint32_t*)(a.k_cache + crow * kAttnD + d0) = kb;
+  // value: raw bf16 from qkv
+  const uint2 vu = *(const uint2*)(row + (size_t)a.HQ * 2 * kAttnD + (size_t)(a.HKV + j) * kAttnD + d0);
+  const float v[4] = {bf16_bits_to_f32(vu.x & 0xFFFFu), bf16_bits_to_f32(vu.x >> 16), bf16_bits_to_f32(vu.y & 0xFFFFu),
+                      bf16_bits_to_f32(vu.y >> 16)};
+  float vm = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) vm = fmaxf(vm, __shfl_xor(vm, o));
+  const float sv = fmaxf(vm, 1e-6f) / kFp8Max;
+  uint32_t vb = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vb |= f32_to_fp8(v[i] / sv) << (8 * i);
+  *(uint32_t*)(a.v_cache + crow * kAttnD + d0) = vb;
+  if (lane == 0) {
+    a.k_scale[crow] = sc;
+    a.v_scale[crow] = sv;
+  }
+}
+
+// ------------------------------------------------------------------ split (flash-decoding)
+
+struct AttnSplitArgs {
+  const uint16_t* q;       // [M, HQ, D] bf16
+  const uint8_t* k_cache;  // [HKV, maxlen, D] fp8
+  const uint8_t* v_cache;
+  const float* k_scale;    // [HKV, maxlen]
+  const float* v_scale;
+  const int64_t* pos;
+  float* m_part;           // [M HQ, NSPLIT]
+  float* l_part;
+  float* acc_part;         // [M HQ, NSPLIT, D]
+  int HQ, HKV, M, maxlen, nsplit;
+  float scale;
+};
+
+__global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kAttnBlk * kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kAttnD * kVPitch];
+  __shared__ float ksc[kAttnBlk], vsc[kAttnBlk];
+  const int j = blockIdx.x / a.nsplit, s = blockIdx.x % a.nsplit;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = a.HQ / a.HKV;
+  const int rows = G * a.M;
+  const int64_t pos = *a.pos;
+  const int64_t L = pos + a.M;
+  const int nblk = (int)((L + kAttnBlk - 1) / kAttnBlk);
+  const int per = (nblk + a.nsplit - 1) / a.nsplit;
+  const int b0 = s * per, b1 = min(b0 + per, nblk);
+  const bool computes = 16 * wave < rows;
+
+  // Q^T operand: lane l holds row 16 wave + l % 16, dims 8 (l / 16) + 32 jj .. + 7
+  const int row = 16 * wave + (lane & 15);
+  const bool rvalid = row < rows;
+  const int qi = rvalid ? row / G : 0;
+  const int hq = j * G + (rvalid ? row % G : 0);
+  uint4 qb[8];
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj)
+    qb[jj] = rvalid ? *(const uint4*)(a.q + ((size_t)qi * a.HQ + hq) * kAttnD + 8 * (lane >> 4) + 32 * jj)
+                    : make_uint4(0, 0, 0, 0);
+  const int64_t qlimit = pos + qi;
+
+  f32x4 acc[16];
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_i = -INFINITY, l_i = 0.f;
+
+  const uint8_t* kb = a.k_cache + (size_t)j * a.maxlen * kAttnD;
+  const uint8_t* vb = a.v_cache + (size_t)j * a.maxlen * kAttnD;
+  // fill roles: K: thread t loads key t / 8, dims 32 (t % 8) .. + 31; V: keys 4 (t % 8) .. + 3,
+  // dims 8 (t / 8) .. + 7
+  const int fk = tid >> 3, fkd = 32 * (tid & 7);
+  const int fv = 4 * (tid & 7), fvd = 8 * (tid >> 3);
+  for (int blk = b0; blk < b1; ++blk) {
+    const int64_t key0 = (int64_t)blk * kAttnBlk;
+    __syncthreads();  // the previous block's LDS reads are done
+    {
+      const int64_t kk = key0 + fk;
+      const bool ok = kk < L;
+      uint4 k0 = make_uint4(0, 0, 0, 0), k1 = k0;
+      float sck = 0.f;
+      if (ok) {
+        const uint4* p = (const uint4*)(kb + (size_t)kk * kAttnD + fkd);
+        k0 = p[0];
+        k1 = p[1];
+        sck = a.k_scale[(size_t)j * a.maxlen + kk];
+      }
+      const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+      uint16_t* dst = Ks + fk * kKPitch + fkd;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        uint32_t o[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const uint32_t w = kw[2 * q4 + h / 2];
+          const uint32_t b0_ = (w >> (16 * (h & 1))) & 0xFF, b1_ = (w >> (16 * (h & 1) + 8)) & 0xFF;
+          o[h] = (uint32_t)f32_to_bf16_bits(fp8_to_f32(b0_) * sck) |
+                 ((uint32_t)f32_to_bf16_bits(fp8_to_f32(b1_) * sck) << 16);
+        }
+        *(uint4*)(dst + 8 * q4) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+      if ((tid & 7) == 0) ksc[fk] = sck;
+    }
+    {
+      uint2 vr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t kk = key0 + fv + i;
+        vr[i] = kk < L ? *(const uint2*)(vb + (size_t)kk * kAttnD + fvd) : make_uint2(0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint32_t b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[i] = ((e < 4 ? vr[i].x : vr[i].y) >> (8 * (e & 3))) & 0xFF;
+        uint2 o;
+        o.x = (uint32_t)f32_to_bf16_bits(fp8_to_f32(b[0])) | ((uint32_t)f32_to_bf16_bits(fp8_to_f32(b[1])) << 16);
+        o.y = (uint32_t)f32_to_bf16_bits(fp8_to_f32(b[2])) | ((uint32_t)f32_to_bf16_bits(fp8_to_f32(b[3])) << 16);
+        *(uint2*)(Vt + (fvd + e) * kVPitch + fv) = o;
+      }
+      if (tid < kAttnBlk) {
+        const int64_t kk = key0 + tid;
+        vsc[tid] = kk < L ? a.v_scale[(size_t)j * a.maxlen + kk] : 0.f;
+      }
+    }
+    __syncthreads();
+    if (!computes) continue;
+    // S^T = K Q^T for the block's two 16-key tiles: lane gets keys 16 kt + 4 (l / 16) + r, row l % 16
+    f32x4 st[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+      const uint16_t* kr = Ks + (16 * kt + (lane & 15)) * kKPitch + 8 * (lane >> 4);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const uint4 kv = *(const uint4*)(kr + 32 * jj);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kv), __builtin_bit_cast(bf16x8, qb[jj]),
+                                                    c, 0, 0, 0);
+      }
+      st[kt] = c;
+    }
+    // mask, online softmax (this lane: one row, 8 keys)
+    float sc[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t kidx = key0 + 16 * kt + 4 * (lane >> 4) + r;
+        const bool allowed = rvalid && kidx < L && kidx <= qlimit;
+        const float v = allowed ? st[kt][r] * a.scale : -INFINITY;
+        sc[4 * kt + r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_i, mx);
+    const float m_safe = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = expf(m_i - m_safe);
+    float psum = 0.f;
+    uint32_t pb[4];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const float p0 = expf(sc[i] - m_safe), p1 = expf(sc[i + 1] - m_safe);
+      psum += p0 + p1;
+      const int k0 = 16 * (i / 4) + 4 * (lane >> 4) + (i & 3);
+      pb[i / 2] = (uint32_t)f32_to_bf16_bits(p0 * vsc[k0]) | ((uint32_t)f32_to_bf16_bits(p1 * vsc[k0 + 1]) << 16);
+    }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    l_i = l_i * alpha + psum;
+    m_i = m_new;
+    // O^T += V^T P^T: k-index 8 (l / 16) + i <-> key 4 (l / 16) + i (i < 4), 16 + 4 (l / 16) + i - 4
+    const bf16x8 pB = __builtin_bit_cast(bf16x8, make_uint4(pb[0], pb[1], pb[2], pb[3]));
+    const int vk = 4 * (lane >> 4);
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      const uint16_t* vr = Vt + (16 * dt + (lane & 15)) * kVPitch;
+      const uint2 lo = *(const uint2*)(vr + vk), hi = *(const uint2*)(vr + 16 + vk);
+      acc[dt] = acc[dt] * alpha;
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y)),
+                                                        pB, acc[dt], 0, 0, 0);
+    }
+  }
+  if (!computes || !rvalid) return;
+  // lanes with l / 16 == 0 .. 3 hold d = 16 dt + 4 (l / 16) + r of row l % 16
+  const size_t h = (size_t)qi * a.HQ + hq;
+  if (lane < 16) {
+    a.m_part[h * a.nsplit + s] = m_i;
+    a.l_part[h * a.nsplit + s] = l_i;
+  }
+  float* ap = a.acc_part + (h * a.nsplit + s) * kAttnD + 4 * (lane >> 4);
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) *(float4*)(ap + 16 * dt) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
+}
+
+// ------------------------------------------------------------------ reduce + output gate
+
+struct AttnReduceArgs {
+  const float* m_part;
+  const float* l_part;
+  const float* acc_part;
+  const uint16_t* qkv;  // [M, QKV] for the gates
+  uint16_t* out;        // [M, HQ D]
+  int HQ, nsplit, ld;
+};
+
+// One workgroup of D threads per (token, query head).
+__global__ __launch_bounds__(kAttnD) void attn_reduce_kernel(AttnReduceArgs a) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  const float* m = a.m_part + (size_t)h * a.nsplit;
+  const float* l = a.l_part + (size_t)h * a.nsplit;
+  float mmax = -INFINITY;
+  for (int s = 0; s < a.nsplit; ++s) mmax = fmaxf(mmax, m[s]);
+  float lt = 0.f, o = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    const float w = m[s] == -INFINITY ? 0.f : expf(m[s] - mmax);
+    lt += w * l[s];
+    o += w * a.acc_part[((size_t)h * a.nsplit + s) * kAttnD + d];
+  }
+  o = bf16r_a(o / lt);
+  const int t = h / a.HQ, hh = h % a.HQ;
+  const float gate = bf16_bits_to_f32(a.qkv[(size_t)t * a.ld + (size_t)hh * 2 * kAttnD + kAttnD + d]);
+  const float g = bf16r_a(1.f / (1.f + expf(-gate)));
+  a.out[(size_t)h * kAttnD + d] = f32_to_bf16_bits(o * g);
+}
+
+}  // namespace tr
+
+using namespace tr;
+
+extern "C" {
+
+size_t tr_attn_workspace_bytes(int M, int HQ, int nsplit) {
+  if (M < 1 || M > kAttnMaxM || HQ < 1 || nsplit < 1) return 0;
+  const size_t rows = (size_t)M * HQ * nsplit;
+  return rows * (2 + kAttnD) * sizeof(float);
+}
+
+int tr_attn_prep(const void* qkv, int ld, const void* q_norm_w, const void* k_norm_w, const void* cos,
+                 const void* sin, int rotary_dim, const int64_t* pos, void* k_cache, void* v_cache, float* k_scale,
+                 float* v_scale, int maxlen, void* q_out, int M, int HQ, int HKV, int D, float eps, void* stream) {
+  if (M == 0) return TR_OK;
+  // rotary_dim: a power of two (its two halves are then an xor-shuffle apart) in [8, D]
+  if (M < 0 || M > kAttnMaxM || D != kAttnD || HQ < 1 || HKV < 1 || HQ % HKV || (rotary_dim & (rotary_dim - 1)) ||
+      rotary_dim < 8 || rotary_dim > D || maxlen < M)
+    return TR_ERR_SHAPE;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos || !sin || !pos || !k_cache || !v_cache || !k_scale || !v_scale || !q_out)
+    return TR_ERR_ARG;
+  if (ld < 2 * HQ * D + 2 * HKV * D) return TR_ERR_ARG;
+  AttnPrepArgs a;
+  a.qkv = (const uint16_t*)qkv;
+  a.qn_w = (const uint16_t*)q_norm_w;
+  a.kn_w = (const uint16_t*)k_norm_w;
+  a.cos = (const uint16_t*)cos;
+  a.sin = (const uint16_t*)sin;
+  a.pos = pos;
+  a.k_cache = (uint8_t*)k_cache;
+  a.v_cache = (uint8_t*)v_cache;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.q_out = (uint16_t*)q_out;
+  a.HQ = HQ;
+  a.HKV = HKV;
+  a.RD = rotary_dim;
+  a.maxlen = maxlen;
+  a.ld = ld;
+  a.eps = eps;
+  hipLaunchKernelGGL(attn_prep_kernel, dim3(HQ + HKV, M), dim3(64), 0, (hipStream_t)stream, a);
+  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, const void* v_cache,
+                   const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos, void* out,
+                   void* workspace, size_t workspace_bytes, int M, int HQ, int HKV, int D, int nsplit, void* stream) {
+  if (M == 0) return TR_OK;
+  if (M < 0 || M > kAttnMaxM || D != kAttnD || HQ < 1 || HKV < 1 || HQ % HKV || (HQ / HKV) * M > 16 * kAttnWaves ||
+      nsplit < 1 || maxlen < M)
+    return TR_ERR_SHAPE;
+  if (!q || !qkv || !k_cache || !v_cache || !k_scale || !v_scale || !pos || !out || !workspace) return TR_ERR_ARG;
+  if (ld < 2 * HQ * D + 2 * HKV * D || workspace_bytes < tr_attn_workspace_bytes(M, HQ, nsplit)) return TR_ERR_ARG;
+  const size_t rows = (size_t)M * HQ * nsplit;
+  AttnSplitArgs s;
+  s.q = (const uint16_t*)q;
+  s.k_cache = (const uint8_t*)k_cache;
+  s.v_cache = (const uint8_t*)v_cache;
+  s.k_scale = k_scale;
+  s.v_scale = v_scale;
+  s.pos = pos;
+  s.m_part = (float*)workspace;
+  s.l_part = s.m_part + rows;
+  s.acc_part = s.l_part + rows;
+  s.HQ = HQ;
+  s.HKV = HKV;
+  s.M = M;
+  s.maxlen = maxlen;
+  s.nsplit = nsplit;
+  s.scale = 1.f / sqrtf((float)D);
+  hipLaunchKernelGGL(attn_split_kernel, dim3(HKV * nsplit), dim3(64 * kAttnWaves), 0, (hipStream_t)stream, s);
+  if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
+  AttnReduceArgs r;
+  r.m_part = s.m_part;
+  r.l_part = s.l_part;
+  r.acc_part = s.acc_part;
+  r.qkv = (const uint16_t*)qkv;
+  r.out = (uint16_t*)out;
+  r.HQ = HQ;
+  r.nsplit = nsplit;
+  r.ld = ld;
+  hipLaunchKernelGGL(attn_reduce_kernel, dim3(M * HQ), dim3(kAttnD), 0, (hipStream_t)stream, r);
+  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+}  // extern "C"

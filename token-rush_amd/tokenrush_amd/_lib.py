@@ -48,6 +48,9 @@ SIGNATURES = {
     "tr_add_rmsnorm": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _I, ctypes.c_float, _I, _P]),
     "tr_silu_mul": (_I, [_P, ctypes.c_long, _P, _I, _I, _P]),
     "tr_gdn_workspace_bytes": (_S, [_I, _I]),
+    "tr_attn_workspace_bytes": (_S, [_I, _I, _I]),
+    "tr_attn_prep": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, ctypes.c_float, _P]),
+    "tr_attn_decode": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P]),
     "tr_gdn_step": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, ctypes.c_long, _P, _P, _P, _P, _P, _S, _I, _I, _I, _I,
                          _I, _I, _I, ctypes.c_float, _P]),
 }

@@ -1,0 +1,111 @@
+"""Full-attention verify step over an FP8 KV cache on gfx950: the reference's tokenrush/fused.py
+attn_prep (fused.py:313-325) and attn_decode_fused (fused.py:448-470) over the HIP kernels of
+csrc/attn.hip.
+
+attn_prep normalises and ropes the M new tokens' queries and keys and writes their keys and
+values into the cache (float8_e4m3fn with one fp32 scale per kv head and position);
+attn_decode_fused is flash-decoding over the live rows (query t sees rows <= pos + t) followed by
+the split combine and the sigmoid output gate. Both are shape-static in the device position, so
+a verify step captures into one hipGraph.
+"""
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+NSPLIT = 32        # key-range splits of the flash-decoding kernel (the reference's default)
+
+
+@dataclass(frozen=True)
+class AttnConfig:
+    """The ModelConfig fields the step reads (tokenrush/config.py:12-16)."""
+    n_heads: int = 24
+    n_kv_heads: int = 4
+    head_dim: int = 256
+    rotary_dim: int = 64
+    rope_theta: float = 1e7
+    eps: float = 1e-6
+
+
+def rope_table(max_pos: int, rotary_dim: int, theta: float, device, dtype=torch.bfloat16):
+    """cos/sin tables [max_pos, rotary_dim] in the activation dtype (tokenrush/ops.py:25-31)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, dtype=torch.float32, device=device) / rotary_dim))
+    pos = torch.arange(max_pos, dtype=torch.float32, device=device)
+    freqs = pos[:, None] * inv_freq[None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def _check_cache(k_cache, v_cache, k_scale, v_scale, cfg):
+    if k_cache.dtype != torch.float8_e4m3fn or v_cache.dtype != torch.float8_e4m3fn:
+        raise RuntimeError("attention: the gfx950 path takes a float8_e4m3fn KV cache with fp32 scales")
+    if k_scale is None or v_scale is None or k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32:
+        raise RuntimeError("attention: fp8 caches need fp32 k_scale and v_scale [HKV, maxlen]")
+    HKV, D = cfg.n_kv_heads, cfg.head_dim
+    if k_cache.dim() != 3 or k_cache.shape[0] != HKV or k_cache.shape[2] != D or v_cache.shape != k_cache.shape:
+        raise RuntimeError("attention: caches must be [HKV, maxlen, D]")
+    if tuple(k_scale.shape) != tuple(k_cache.shape[:2]) or tuple(v_scale.shape) != tuple(k_cache.shape[:2]):
+        raise RuntimeError("attention: scales must be [HKV, maxlen]")
+    for t in (k_cache, v_cache, k_scale, v_scale):
+        if not t.is_contiguous():
+            raise RuntimeError("attention: caches and scales must be contiguous")
+
+
+def attn_prep(qkv, q_norm_w, k_norm_w, cos, sin, pos_t, k_cache, v_cache, cfg, k_scale=None, v_scale=None):
+    """qkv [M, HQ 2D + 2 HKV D] bf16 -> q [M, HQ D] bf16, normed and roped; writes the new keys
+    and values into cache rows pos..pos+M-1 (fused.py:313-325)."""
+    _lib.require_gpu(qkv, q_norm_w, k_norm_w, cos, sin, pos_t, k_cache, v_cache)
+    _check_cache(k_cache, v_cache, k_scale, v_scale, cfg)
+    if qkv.dtype != torch.bfloat16 or qkv.stride(1) != 1:
+        raise RuntimeError("attn_prep: qkv must be bf16 with unit column stride")
+    if pos_t.dtype != torch.int64 or cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16:
+        raise RuntimeError("attn_prep: int64 pos_t and bf16 cos/sin tables")
+    if cos.shape[1] != cfg.rotary_dim or not (cos.is_contiguous() and sin.is_contiguous()):
+        raise RuntimeError("attn_prep: cos/sin must be contiguous [max_pos, rotary_dim]")
+    M = qkv.shape[0]
+    HQ, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    q = torch.empty(M, HQ * D, device=qkv.device, dtype=torch.bfloat16)
+    ld = qkv.stride(0) if M > 1 else qkv.shape[1]
+    rc = _lib.lib().tr_attn_prep(_lib.ptr(qkv), ld, _lib.ptr(q_norm_w), _lib.ptr(k_norm_w), _lib.ptr(cos),
+                                 _lib.ptr(sin), cfg.rotary_dim, _lib.ptr(pos_t), _lib.ptr(k_cache), _lib.ptr(v_cache),
+                                 _lib.ptr(k_scale), _lib.ptr(v_scale), k_cache.shape[1], _lib.ptr(q), M, HQ, HKV, D,
+                                 float(cfg.eps), _lib.stream_of(qkv))
+    _lib.check(rc, "tr_attn_prep")
+    return q
+
+
+_ws = {}
+
+
+def workspace(M: int, HQ: int, nsplit: int, device):
+    need = int(_lib.lib().tr_attn_workspace_bytes(M, HQ, nsplit))
+    if need == 0:
+        raise RuntimeError(f"attention workspace: unsupported M={M}")
+    key = torch.device(device).index or 0
+    ws = _ws.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
+        _ws[key] = ws
+    return ws
+
+
+def attn_decode_fused(q, qkv, k_cache, v_cache, pos_t, cfg, k_scale=None, v_scale=None, NSPLIT=NSPLIT):
+    """q [M, HQ D] (from attn_prep) for the M new tokens at pos.., qkv [M, ..] (for the gates)
+    -> gated attention output [M, HQ D] bf16; query t sees cache rows <= pos + t
+    (fused.py:448-470)."""
+    _lib.require_gpu(q, qkv, k_cache, v_cache, pos_t)
+    _check_cache(k_cache, v_cache, k_scale, v_scale, cfg)
+    if q.dtype != torch.bfloat16 or not q.is_contiguous() or qkv.dtype != torch.bfloat16 or qkv.stride(1) != 1:
+        raise RuntimeError("attn_decode_fused: bf16 q (contiguous) and qkv")
+    M = q.shape[0]
+    HQ, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    out = torch.empty(M, HQ * D, device=q.device, dtype=torch.bfloat16)
+    ws = workspace(M, HQ, NSPLIT, q.device)
+    ld = qkv.stride(0) if M > 1 else qkv.shape[1]
+    rc = _lib.lib().tr_attn_decode(_lib.ptr(q), _lib.ptr(qkv), ld, _lib.ptr(k_cache), _lib.ptr(v_cache),
+                                   _lib.ptr(k_scale), _lib.ptr(v_scale), k_cache.shape[1], _lib.ptr(pos_t),
+                                   _lib.ptr(out), _lib.ptr(ws), ws.numel(), M, HQ, HKV, D, NSPLIT,
+                                   _lib.stream_of(q))
+    _lib.check(rc, "tr_attn_decode")
+    return out
