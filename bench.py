@@ -18,8 +18,8 @@ roofline    the dominant kernel (gate/up, 53% of the bytes): its algorithmic byt
 accept      on-device accept latency (BASELINE config 3 and 4): mean per launch over a graph of
             back-to-back calls.
 config5     one verify step of the random-init 64-layer hybrid at M = 8 (257 int4 GEMMs, split-K
-            partial consumers, stand-in mixers, lm_head, greedy accept) captured as one hipGraph;
-            time per replay and weight bytes / time.
+            partial consumers, 48 GDN steps, 16 FP8 attention layers over 8192 live tokens, lm_head,
+            greedy accept) captured as one hipGraph; time per replay and weight bytes / time.
 cpu_baseline  the reference's CPU path restated in torch (unpack, in-place dequant, F.linear) on
             one layer set at M = 8, OMP_NUM_THREADS host cores, median of >= 5 passes
             (about 10 s).
@@ -145,8 +145,8 @@ def accept_latency(torch, dev):
 
 def config5_step(torch, dev, M=M_VERIFY, reps=10):
     """one verify step of the random-init 64-layer hybrid (48 GDN + 16 attention
-    layers, int4 g128 weights, stand-in mixers) + lm_head + greedy accept/commit, captured as one
-    hipGraph (tokenrush_amd.step). Returns the replay time and the weight-streaming rate."""
+    layers, int4 g128 weights, GDN steps and FP8 attention over 8192 live tokens) + lm_head + greedy
+    accept/commit, captured as one hipGraph (tokenrush_amd.step). Returns the replay time and the weight-streaming rate."""
     from tokenrush_amd.accept import AcceptState
     from tokenrush_amd.step import StepConfig, VerifyModel, prepare
     t0 = time.perf_counter()
@@ -157,19 +157,24 @@ def config5_step(torch, dev, M=M_VERIFY, reps=10):
     x0 = torch.randn(M, model.cfg.hidden, device=dev, generator=gen).to(torch.bfloat16)
     spec = torch.randint(0, model.cfg.vocab, (M,), device=dev, generator=gen)
     st = AcceptState(M, dev)
+    st.pos.fill_(model.cfg.live)               # the cache holds `live` tokens; the accept advances pos
+    st.slot.zero_()
     g = graph_of(torch, lambda: model.step(x0, spec, st))
     build_s = time.perf_counter() - t0
     t = timed_graph(torch, g, reps=reps)
-    nbytes = model.nbytes()
-    launches = model.cfg.n_layers * 7 + 2
+    nbytes, state_bytes, live = model.nbytes(), model.state.nbytes(), model.cfg.live
+    n_attn = sum(1 for li in range(model.cfg.n_layers) if model.cfg.is_attention(li))
+    launches = (model.cfg.n_layers - n_attn) * 7 + n_attn * 9 + 2
     del g, model
     torch.cuda.empty_cache()
     return {"ms_per_step": round(t * 1e3, 3), "weights_GB": round(nbytes / 1e9, 3),
             "weight_GBps": round(nbytes / t / 1e9, 1), "launches": launches, "M": M, "replays": reps,
             "build_s": round(build_s, 1),
+            "state_GB": round(state_bytes / 1e9, 3), "live_tokens": live,
             "note": "one hipGraph: 257 int4 GEMMs (the 64 gate/up with silu_mul in the epilogue), 129 add_rmsnorm "
-                    "(split-K partial consumers), 64 stand-in mixers, lm_head 248320x5120 with the greedy accept/commit "
-                    "in its epilogue"}
+                    "(split-K partial consumers), 48 GDN steps (conv ring, delta rule, 8 snapshot slots, gated norm), "
+                    "16 attention layers (prep + FP8 flash-decoding split + combine) over 8192 live tokens, lm_head "
+                    "248320x5120 with the greedy accept/commit in its epilogue"}
 
 
 def cpu_baseline(M=M_VERIFY, min_reps=5, budget_s=10.0):

@@ -192,9 +192,9 @@ int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* strea
 
 /* ---------------------------------------------------------------- GDN (gated delta rule) step */
 
-/* Bytes of the workspace tr_gdn_step needs for M tokens and HV value heads (0 if unsupported).
- * Zero-filled once by the caller; every call leaves its counters at zero. */
-size_t tr_gdn_workspace_bytes(int M, int HV);
+/* Bytes of the workspace tr_gdn_step needs for M tokens, H key heads and HV value heads (0 if
+ * unsupported). Zero-filled once by the caller; every call leaves its counters at zero. */
+size_t tr_gdn_workspace_bytes(int M, int H, int HV);
 
 /* One M-token (1..8) GDN step of one layer: causal conv (kernel 4) over the ring with silu, b/a gates
  * from x . ba_w, L2-normalised q and k, the gated delta rule with the state after token t written to
@@ -203,7 +203,8 @@ size_t tr_gdn_workspace_bytes(int M, int HV);
  *   bf16, ring [2 H K + HV V, R] bf16 (columns (pos + t) % R updated), conv_w [2 H K + HV V, 4] bf16,
  *   A and dt_bias [HV] fp32, rec fp32 slots slot_stride floats apart, each [HV, K, V]; the committed
  *   state is slot *slot (device int64); pos: device int64 position of token 0; norm_w [V] bf16;
- *   y [M, HV V] bf16. K == V == 128, HV % H == 0, R >= M + 3, hidden % 8 == 0.
+ *   y [M, HV V] bf16. K == V == 128, HV % H == 0, R >= M + 3, hidden % 32 == 0. Two launches: the
+ *   conv + gates of all heads, then the recurrence per (value head, 32-column block).
  * Replaces: gdn_step_fused (tokenrush/fused.py:119-236: _gdn_step_fused_kernel + _gated_norm_kernel),
  * the fused path of gdn_forward (tokenrush/model.py:76-80). */
 int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void* ring, const void* conv_w,

@@ -1,12 +1,16 @@
-"""The verify-step driver (tokenrush_amd/step.py) on a small hybrid config: the body against a
-torch float reference built from the same weights (dequantized by the bit-exact HIP dequant),
-the greedy accept against the oracle on the step's own logits (bit-exact), and the whole step
-captured as one hipGraph reproducing the eager step bit-for-bit on repeated replays."""
+"""The verify-step driver (tokenrush_amd/step.py) on a small hybrid config (3 GDN layers and one
+attention layer with the config-5 head geometry, 300 live cache rows): the body against a float
+reference built from the same weights and state (exact int4 weights, fp32 matmuls, the oracle's
+GDN step and FP8 attention), the greedy accept against the oracle on the step's own logits
+(bit-exact), and the whole step captured as one hipGraph reproducing the eager step bit-for-bit on
+repeated replays from the same state."""
 import numpy as np
 import pytest
 import torch
 
 from oracle import accept as oa
+from oracle import attn as oat
+from oracle import gdn as og
 
 pytestmark = pytest.mark.gpu
 
@@ -29,18 +33,36 @@ def _ref_body(model, x0):
 
     def silu_mul(u):
         F = u.shape[1] // 2
-        g, v = u[:, :F], u[:, F:2 * F]
-        return bf(g / (1 + torch.exp(-g)) * v)
+        gg, v = u[:, :F], u[:, F:2 * F]
+        return bf(gg / (1 + torch.exp(-gg)) * v)
 
+    st = model.state
+    npf = lambda t: t.float().cpu().numpy()
+    pos, slot = int(st.pos), int(st.slot)
+    ring, rec = npf(st.ring), npf(st.rec)
+    kc, vc = st.k.view(torch.uint8).cpu().numpy(), st.v.view(torch.uint8).cpu().numpy()
+    ks, vs, cos, sin = npf(st.k_scale), npf(st.v_scale), npf(st.cos), npf(st.sin)
+    g = cfg.gdn
     x = x0.float()
     h = None
-    for L in model.layers:
+    for li, L in enumerate(model.layers):
         if h is not None:
             x = bf(x + bf(h))
         n = norm(x, L.ln1)
         u = bf(lin(L.proj, n))
-        y = silu_mul(u[:, :2 * cfg.mixer_out])
-        h = lin(L.out, y)
+        if L.attention:
+            a = model.attn_index[li]
+            q, kc[a], vc[a], ks[a], vs[a] = oat.attn_prep(npf(u), npf(L.q_norm_w), npf(L.k_norm_w), cos, sin, pos,
+                                                          kc[a], vc[a], ks[a], vs[a], cfg.n_heads, cfg.n_kv_heads,
+                                                          cfg.head_dim, cfg.rotary_dim, cfg.eps)
+            y = oat.attn_decode(q, npf(u), kc[a], vc[a], ks[a], vs[a], pos, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim)
+        else:
+            k = model.gdn_index[li]
+            y, ring[k], rec_k = og.gdn_step(npf(u), npf(n), npf(L.in_ba), ring[k], npf(L.conv_w), npf(L.A),
+                                            npf(L.dt_bias), rec[:, k], slot, npf(L.norm_w), pos, g.gdn_k_heads,
+                                            g.gdn_v_heads, g.gdn_k_dim, g.gdn_v_dim, cfg.eps)
+            rec[:, k] = rec_k
+        h = lin(L.out, torch.from_numpy(y).to(x.device))
         x = bf(x + bf(h))
         n = norm(x, L.ln2)
         a = silu_mul(bf(lin(L.gate_up, n)))
@@ -53,7 +75,9 @@ def _ref_body(model, x0):
 @pytest.fixture(scope="module")
 def small_model(dev):
     from tokenrush_amd.step import SMALL, VerifyModel
-    return VerifyModel(SMALL, seed=3)
+    m = VerifyModel(SMALL, seed=3)
+    m.initial_state = m.state.snapshot()
+    return m
 
 
 @pytest.mark.parametrize("M", [1, 8])
@@ -62,8 +86,9 @@ def test_body_matches_float_reference(small_model, M):
     m = small_model
     g = torch.Generator(device="cuda:0").manual_seed(M)
     x0 = torch.randn(M, m.cfg.hidden, device="cuda:0", generator=g).to(torch.bfloat16)
-    got = m.body(x0).float()
+    m.state.restore(m.initial_state)
     ref = _ref_body(m, x0)
+    got = m.body(x0).float()
     rel = ((got - ref).norm() / ref.norm()).item()
     assert rel < 2e-2, rel
 
@@ -76,7 +101,15 @@ def test_step_accept_and_graph_replay(small_model):
     g = torch.Generator(device="cuda:0").manual_seed(11)
     x0 = torch.randn(M, m.cfg.hidden, device="cuda:0", generator=g).to(torch.bfloat16)
     st = AcceptState(M, "cuda:0")
+    live = m.cfg.live
+
+    def reset():
+        m.state.restore(m.initial_state)
+        st.pos.fill_(live)
+        st.slot.zero_()
+
     # drafts: the target's own argmax on a prefix of 3, then a wrong token
+    reset()
     logits = m.body(x0)
     pred = logits.float().argmax(-1).cpu().numpy()
     spec = np.zeros(M, dtype=np.int64)
@@ -84,11 +117,11 @@ def test_step_accept_and_graph_replay(small_model):
     spec[1:4] = pred[0:3]
     spec[4:] = (pred[3:7] + 1) % m.cfg.vocab
     spec_t = torch.from_numpy(spec).to("cuda:0")
-    st.pos.fill_(100)
+    reset()
     lg = m.step(x0, spec_t, st)
     torch.cuda.synchronize()
     lg_np = lg.view(torch.int16).cpu().numpy().view(np.uint16)
-    want = oa.verify_chain(oa.argmax_rows(oa.logits_f32(lg_np)), spec, pos=100)
+    want = oa.verify_chain(oa.argmax_rows(oa.logits_f32(lg_np)), spec, pos=live)
     assert int(st.n_accepted) == want["n"] >= 3 and int(st.tok) == want["tok"] and int(st.pos) == want["pos"]
     eager = (lg.clone(), st.n_accepted.clone(), st.tok.clone(), st.slot.clone(), st.tokens.clone(), st.commit.clone())
 
@@ -96,14 +129,15 @@ def test_step_accept_and_graph_replay(small_model):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        st.pos.fill_(100)
+        reset()
         m.step(x0, spec_t, st)                     # warm-up on the capture stream
     torch.cuda.current_stream().wait_stream(side)
     with torch.cuda.graph(graph):
         lg_g = m.step(x0, spec_t, st)
     for rep in range(3):
-        st.pos.fill_(100)
+        reset()
         st.n_accepted.fill_(-1)
+        torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
         _ = m.body(x0)                              # eager work between replays

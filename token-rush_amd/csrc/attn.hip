@@ -32,6 +32,7 @@ constexpr int kAttnWaves = 4;
 constexpr int kKPitch = kAttnD + 8;     // bf16 elements per K row in LDS
 constexpr int kVPitch = kAttnBlk + 4;   // bf16 elements per V^T row (one d) in LDS
 constexpr float kFp8Max = 448.f;
+constexpr int kMaxSplit = 256;  // key-range splits of one flash-decoding call
 
 // ------------------------------------------------------------------ fp8 e4m3fn (OCP) helpers
 
@@ -210,27 +211,45 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
   for (int dt = 0; dt < 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_i = -INFINITY, l_i = 0.f;
 
-  const uint8_t* kb = a.k_cache + (size_t)j * a.maxlen * kAttnD;
-  const uint8_t* vb = a.v_cache + (size_t)j * a.maxlen * kAttnD;
+  // Cache reads go through buffer resources sized to the L live rows: rows past them, and the
+  // prefetch past the split's last block, read zeros with no memory access and no branch.
+  const int liveL = (int)L;
+  const auto krs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_cache + (size_t)j * a.maxlen * kAttnD), (short)0,
+                                                     liveL * kAttnD, 0x00020000);
+  const auto vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_cache + (size_t)j * a.maxlen * kAttnD), (short)0,
+                                                     liveL * kAttnD, 0x00020000);
+  const auto ksr = __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_scale + (size_t)j * a.maxlen), (short)0, liveL * 4,
+                                                     0x00020000);
+  const auto vsr = __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_scale + (size_t)j * a.maxlen), (short)0, liveL * 4,
+                                                     0x00020000);
+  constexpr int kOob = 0x7FFFFFF0;
   // fill roles: K: thread t loads key t / 8, dims 32 (t % 8) .. + 31; V: keys 4 (t % 8) .. + 3,
-  // dims 8 (t / 8) .. + 7
+  // dims 8 (t / 8) .. + 7; scales: threads 0..31 (V) and every 8th thread (K)
   const int fk = tid >> 3, fkd = 32 * (tid & 7);
   const int fv = 4 * (tid & 7), fvd = 8 * (tid >> 3);
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  u4 pk0, pk1;
+  u2 pv[4];
+  float psk, psv;
+  auto fetch = [&](int blk, bool on) {
+    const int key0 = blk * kAttnBlk;
+    const int kk = key0 + fk;
+    pk0 = __builtin_amdgcn_raw_buffer_load_b128(krs, on ? kk * kAttnD + fkd : kOob, 0, 0);
+    pk1 = __builtin_amdgcn_raw_buffer_load_b128(krs, on ? kk * kAttnD + fkd + 16 : kOob, 0, 0);
+    psk = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ksr, on ? kk * 4 : kOob, 0, 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      pv[i] = __builtin_amdgcn_raw_buffer_load_b64(vrs, on ? (key0 + fv + i) * kAttnD + fvd : kOob, 0, 0);
+    psv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vsr, on && tid < kAttnBlk ? (key0 + tid) * 4 : kOob, 0, 0));
+  };
+  fetch(b0, b0 < b1);
   for (int blk = b0; blk < b1; ++blk) {
     const int64_t key0 = (int64_t)blk * kAttnBlk;
     __syncthreads();  // the previous block's LDS reads are done
     {
-      const int64_t kk = key0 + fk;
-      const bool ok = kk < L;
-      uint4 k0 = make_uint4(0, 0, 0, 0), k1 = k0;
-      float sck = 0.f;
-      if (ok) {
-        const uint4* p = (const uint4*)(kb + (size_t)kk * kAttnD + fkd);
-        k0 = p[0];
-        k1 = p[1];
-        sck = a.k_scale[(size_t)j * a.maxlen + kk];
-      }
-      const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+      const uint32_t kw[8] = {pk0.x, pk0.y, pk0.z, pk0.w, pk1.x, pk1.y, pk1.z, pk1.w};
+      const float sck = psk;
       uint16_t* dst = Ks + fk * kKPitch + fkd;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
@@ -247,27 +266,19 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
       if ((tid & 7) == 0) ksc[fk] = sck;
     }
     {
-      uint2 vr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t kk = key0 + fv + i;
-        vr[i] = kk < L ? *(const uint2*)(vb + (size_t)kk * kAttnD + fvd) : make_uint2(0, 0);
-      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         uint32_t b[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) b[i] = ((e < 4 ? vr[i].x : vr[i].y) >> (8 * (e & 3))) & 0xFF;
+        for (int i = 0; i < 4; ++i) b[i] = ((e < 4 ? pv[i].x : pv[i].y) >> (8 * (e & 3))) & 0xFF;
         uint2 o;
         o.x = (uint32_t)f32_to_bf16_bits(fp8_to_f32(b[0])) | ((uint32_t)f32_to_bf16_bits(fp8_to_f32(b[1])) << 16);
         o.y = (uint32_t)f32_to_bf16_bits(fp8_to_f32(b[2])) | ((uint32_t)f32_to_bf16_bits(fp8_to_f32(b[3])) << 16);
         *(uint2*)(Vt + (fvd + e) * kVPitch + fv) = o;
       }
-      if (tid < kAttnBlk) {
-        const int64_t kk = key0 + tid;
-        vsc[tid] = kk < L ? a.v_scale[(size_t)j * a.maxlen + kk] : 0.f;
-      }
+      if (tid < kAttnBlk) vsc[tid] = psv;
     }
+    fetch(blk + 1, blk + 1 < b1);  // the next block's loads run under this block's compute
     __syncthreads();
     if (!computes) continue;
     // S^T = K Q^T for the block's two 16-key tiles: lane gets keys 16 kt + 4 (l / 16) + r, row l % 16
@@ -352,17 +363,39 @@ struct AttnReduceArgs {
 
 // One workgroup of D threads per (token, query head).
 __global__ __launch_bounds__(kAttnD) void attn_reduce_kernel(AttnReduceArgs a) {
+  __shared__ float wsh[kMaxSplit], lsh;
   const int h = blockIdx.x, d = threadIdx.x;
-  const float* m = a.m_part + (size_t)h * a.nsplit;
-  const float* l = a.l_part + (size_t)h * a.nsplit;
-  float mmax = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) mmax = fmaxf(mmax, m[s]);
-  float lt = 0.f, o = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const float w = m[s] == -INFINITY ? 0.f : expf(m[s] - mmax);
-    lt += w * l[s];
-    o += w * a.acc_part[((size_t)h * a.nsplit + s) * kAttnD + d];
+  // split weights exp(m_s - max) once per workgroup (fixed order), then each thread sums its
+  // dimension over the splits with all loads issued ahead
+  if (d < 64) {
+    float mm = -INFINITY;
+    for (int s = d; s < a.nsplit; s += 64) mm = fmaxf(mm, a.m_part[(size_t)h * a.nsplit + s]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+    for (int s = d; s < a.nsplit; s += 64) {
+      const float m = a.m_part[(size_t)h * a.nsplit + s];
+      wsh[s] = m == -INFINITY ? 0.f : expf(m - mm);
+    }
   }
+  __syncthreads();
+  if (d == 0) {
+    float lt = 0.f;
+    for (int s = 0; s < a.nsplit; ++s) lt += wsh[s] * a.l_part[(size_t)h * a.nsplit + s];
+    lsh = lt;
+  }
+  const float* ap = a.acc_part + (size_t)h * a.nsplit * kAttnD + d;
+  float o = 0.f;
+  int s = 0;
+  for (; s + 8 <= a.nsplit; s += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = ap[(size_t)(s + i) * kAttnD];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o += wsh[s + i] * v[i];
+  }
+  for (; s < a.nsplit; ++s) o += wsh[s] * ap[(size_t)s * kAttnD];
+  __syncthreads();
+  const float lt = lsh;
   o = bf16r_a(o / lt);
   const int t = h / a.HQ, hh = h % a.HQ;
   const float gate = bf16_bits_to_f32(a.qkv[(size_t)t * a.ld + (size_t)hh * 2 * kAttnD + kAttnD + d]);
@@ -420,7 +453,7 @@ int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, 
                    void* workspace, size_t workspace_bytes, int M, int HQ, int HKV, int D, int nsplit, void* stream) {
   if (M == 0) return TR_OK;
   if (M < 0 || M > kAttnMaxM || D != kAttnD || HQ < 1 || HKV < 1 || HQ % HKV || (HQ / HKV) * M > 16 * kAttnWaves ||
-      nsplit < 1 || maxlen < M)
+      nsplit < 1 || nsplit > kMaxSplit || maxlen < M)
     return TR_ERR_SHAPE;
   if (!q || !qkv || !k_cache || !v_cache || !k_scale || !v_scale || !pos || !out || !workspace) return TR_ERR_ARG;
   if (ld < 2 * HQ * D + 2 * HKV * D || workspace_bytes < tr_attn_workspace_bytes(M, HQ, nsplit)) return TR_ERR_ARG;

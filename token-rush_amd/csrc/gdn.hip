@@ -19,23 +19,30 @@
 // The committed state is read from slot *slot of rec; the state after token t is written to
 // slot t, so the accept can commit any prefix by naming its slot (tokenrush/state.py:30-39).
 //
-// Layout and work split (MI355X): one 64-lane wave per (value head, 32-column block of V), so
-// a layer's 48 x 4 = 192 workgroups spread the 64 KB-per-head state over the CUs. Lane
-// (vq = lane % 8, kg = lane / 8) holds S[16 kg .. 16 kg + 15][4 vq .. 4 vq + 3] of its block in
-// registers for all M tokens; its snapshot stores are 16-byte vectors, 8 lanes per 128-byte row
-// segment. Sums over k combine each lane's 16 rows, then lanes kg = 0..7 by xor shuffles. The
-// conv outputs of all M tokens (128 q, 128 k and 32 v channels) are computed up front into LDS.
-// The gated norm needs the whole head: the four column blocks store bf16 o to a workspace with
-// agent-scope stores, and the last of them to arrive normalizes the head for every token.
+// Two launches on MI355X:
+//   gdn_prep_kernel does the work every column block of a head shares, once: the conv of all
+//   channels for the M tokens (one thread per channel; the ring update), the L2 normalisation
+//   of q and k (a 256-channel workgroup holds two whole heads), and the gate dot products
+//   (one workgroup per gate row, the four waves splitting the hidden dim).
+//   gdn_step_kernel runs the recurrence, one workgroup of four waves per (value head, 32-column
+//   block): 48 x 4 = 192 workgroups, so the M x 64 KB-per-head snapshot stores -- the kernel's
+//   cost -- spread over most CUs. Wave w holds rows 32 w .. 32 w + 31 of the block's [128 x 32]
+//   state tile; lane (vq = l % 8, kg = l / 8) holds rows 32 w + 4 kg .. + 3, columns 4 vq .. + 3,
+//   in registers for all M tokens, and its snapshot stores are 16-byte vectors, 8 lanes per
+//   128-byte row segment. Sums over k: a lane's 4 rows, the wave's 8 row groups (DPP / permlane
+//   steps) and the 4 waves (LDS, fixed order), once per token for both o_t and kv_{t+1}.
+//   The gated norm needs the whole head: the four blocks store bf16 o with agent-scope stores,
+//   and the last of them to arrive normalizes the head for every token.
 #include "accept_common.h"
 
 namespace tr {
 
 constexpr int kGdnK = 128;   // key head dim
 constexpr int kGdnV = 128;   // value head dim
-constexpr int kGdnBV = 32;   // value columns per workgroup
+constexpr int kGdnBV = 32;   // value columns per step workgroup
 constexpr int kGdnNVB = kGdnV / kGdnBV;
 constexpr int kGdnMaxM = 8;  // tokens per step (the reference's MP, fused.py:150)
+constexpr int kGdnThreads = 256;
 
 struct GdnArgs {
   const uint16_t* qkvz;    // [M, ld] bf16: q | k | v | z
@@ -50,202 +57,280 @@ struct GdnArgs {
   const int64_t* pos;      // [1] position of token 0
   const uint16_t* norm_w;  // [V] bf16
   uint16_t* y;             // [M, HV V] bf16
-  float* o_ws;             // [M, HV V] fp32 (bf16 values), workspace
+  float* o_ws;             // [M, HV V] fp32 (bf16 values), workspace: head outputs for the norm
   int* cnt;                // [HV] arrival counters, one per 128-byte line, zero between calls
+  float* qk;               // [M, 2 H K] fp32, workspace: normalised q (times K^-1/2) | k
+  uint16_t* vconv;         // [M, HV V] bf16, workspace: conv + silu of the v channels
+  float* gates;            // [M, 2 HV] fp32 (bf16 values), workspace: b | a
   long slot_stride;        // floats
   int ld, hidden, M, H, HV, R;
   float eps, scale;
 };
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
-
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-// Sum over the 8 lanes that share lane % 8 (kg = 0..7), in a fixed order for every lane.
-__device__ __forceinline__ float kg_sum(float v) {
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
-}
-
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : logf(1.f + expf(x)); }
 
-__global__ __launch_bounds__(64) void gdn_step_kernel(GdnArgs a) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gdn_rsrc(const void* p, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
+}
+
+// ------------------------------------------------------------------ prep: conv, norms, gates
+
+__global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
+  __shared__ float part[4][kGdnMaxM];
+  __shared__ float ssq[4][kGdnMaxM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int M = a.M;
+  const int QK = a.H * kGdnK;
+  const int C = 2 * QK + a.HV * kGdnV;
+  const int n_conv = (C + kGdnThreads - 1) / kGdnThreads;
+  if ((int)blockIdx.x < n_conv) {
+    // one conv channel per thread; a workgroup's 256 channels are two whole q or k heads (QK is
+    // a multiple of 256) or 256 v channels
+    const int ch = blockIdx.x * kGdnThreads + tid;
+    const bool on = ch < C;
+    const int pr = (int)(*a.pos % a.R);  // ring column of token 0
+    float y[kGdnMaxM];
+#pragma unroll
+    for (int t = 0; t < kGdnMaxM; ++t) y[t] = 0.f;
+    if (on) {
+      const uint2 wu = *(const uint2*)(a.conv_w + (size_t)ch * 4);
+      const float w0 = bf16_bits_to_f32(wu.x & 0xFFFFu), w1 = bf16_bits_to_f32(wu.x >> 16);
+      const float w2 = bf16_bits_to_f32(wu.y & 0xFFFFu), w3 = bf16_bits_to_f32(wu.y >> 16);
+      uint16_t* rrow = a.ring + (size_t)ch * a.R;
+      float win[kGdnMaxM + 3];
+      uint16_t xin[kGdnMaxM];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) win[j] = bf16_bits_to_f32(rrow[(pr + j - 3 + a.R) % a.R]);
+#pragma unroll
+      for (int t = 0; t < kGdnMaxM; ++t) {
+        xin[t] = t < M ? a.qkvz[(size_t)t * a.ld + ch] : (uint16_t)0;
+        win[t + 3] = bf16_bits_to_f32(xin[t]);
+      }
+#pragma unroll
+      for (int t = 0; t < kGdnMaxM; ++t) {
+        if (t < M) {
+          float yv = win[t] * w0;
+          yv = yv + win[t + 1] * w1;
+          yv = yv + win[t + 2] * w2;
+          yv = yv + win[t + 3] * w3;
+          yv = bf16r(yv);
+          y[t] = bf16r(yv / (1.f + expf(-yv)));
+        }
+      }
+      for (int t = 0; t < M; ++t) rrow[(pr + t) % a.R] = xin[t];
+    }
+    if ((int)blockIdx.x * kGdnThreads >= 2 * QK) {  // v channels: stored as they are
+      if (on)
+        for (int t = 0; t < M; ++t) a.vconv[(size_t)t * a.HV * kGdnV + (ch - 2 * QK)] = f32_to_bf16_bits(y[t]);
+      return;
+    }
+    // q or k: normalise each token's 128-channel head (waves 0-1: first head, 2-3: second)
+#pragma unroll
+    for (int t = 0; t < kGdnMaxM; ++t) {
+      const float s = sum_wave(y[t] * y[t]);
+      if (lane == 0) ssq[wave][t] = s;
+    }
+    __syncthreads();
+    const bool isq = ch < QK;
+    const int hb = wave & ~1;  // first wave of this head
+    for (int t = 0; t < M; ++t) {
+      const float n = sqrtf((ssq[hb][t] + ssq[hb + 1][t]) + 1e-6f);
+      a.qk[(size_t)t * 2 * QK + ch] = isq ? y[t] / n * a.scale : y[t] / n;
+    }
+    return;
+  }
+  // gate row r of ba_w: b for r < HV, a for r >= HV
+  const int r = blockIdx.x - n_conv;
+  const int q0 = a.hidden / 4 * wave, q1 = a.hidden / 4 * (wave + 1);
+  const auto xr = gdn_rsrc(a.x, (size_t)M * a.hidden * 2);
+  const uint16_t* wrow = a.ba_w + (size_t)r * a.hidden;
+  float acc[kGdnMaxM];
+#pragma unroll
+  for (int t = 0; t < kGdnMaxM; ++t) acc[t] = 0.f;
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  for (int e = q0 + 8 * lane; e < q1; e += 8 * 64 * 2) {
+    // two chunks per iteration, every load issued before the arithmetic
+    const int e1 = e + 8 * 64;
+    const bool in1 = e1 < q1;
+    const uint4 w0v = *(const uint4*)(wrow + e);
+    const uint4 w1v = in1 ? *(const uint4*)(wrow + e1) : make_uint4(0, 0, 0, 0);
+    u4 x0[kGdnMaxM], x1[kGdnMaxM];
+#pragma unroll
+    for (int t = 0; t < kGdnMaxM; ++t) {
+      x0[t] = __builtin_amdgcn_raw_buffer_load_b128(xr, t < M ? (t * a.hidden + e) * 2 : 0x7FFFFFF0, 0, 0);
+      x1[t] = __builtin_amdgcn_raw_buffer_load_b128(xr, (t < M && in1) ? (t * a.hidden + e1) * 2 : 0x7FFFFFF0, 0, 0);
+    }
+    const uint32_t wa[8] = {w0v.x, w0v.y, w0v.z, w0v.w, w1v.x, w1v.y, w1v.z, w1v.w};
+#pragma unroll
+    for (int t = 0; t < kGdnMaxM; ++t) {
+      const uint32_t xw[8] = {x0[t].x, x0[t].y, x0[t].z, x0[t].w, x1[t].x, x1[t].y, x1[t].z, x1[t].w};
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        acc[t] += bf16_bits_to_f32(xw[c] & 0xFFFFu) * bf16_bits_to_f32(wa[c] & 0xFFFFu) +
+                  bf16_bits_to_f32(xw[c] >> 16) * bf16_bits_to_f32(wa[c] >> 16);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kGdnMaxM; ++t) {
+    const float v = sum_wave(acc[t]);
+    if (lane == 0) part[wave][t] = v;
+  }
+  __syncthreads();
+  if (tid < M) a.gates[(size_t)tid * 2 * a.HV + r] = bf16r(((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid]);
+}
+
+// ------------------------------------------------------------------ step: the recurrence
+
+__global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   __shared__ float cq[kGdnMaxM][kGdnK], ck[kGdnMaxM][kGdnK], cv[kGdnMaxM][kGdnBV];
+  __shared__ float beta_s[kGdnMaxM], decay_s[kGdnMaxM];
+  __shared__ float4 red[2][4][8], red_n[2][4][8];
   __shared__ int last;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hv = blockIdx.x / kGdnNVB, vb = blockIdx.x % kGdnNVB;
   const int ih = hv / (a.HV / a.H);
   const int M = a.M;
   const int QK = a.H * kGdnK, VAL = a.HV * kGdnV;
-  const int64_t pos = *a.pos;
   const int64_t slot = *a.slot;
   const int vq = lane & 7, kg = lane >> 3;
-  const int v0 = vb * kGdnBV + 4 * vq;  // this lane's first column within the head
+  const int c0 = 4 * vq;                    // this lane's first column within the block
+  const int v0 = vb * kGdnBV + c0;          // ... within the head
+  const int k0 = 32 * wave + 4 * kg;        // this lane's first row
 
-  // Committed state tile, loaded first: everything below overlaps its latency.
-  float4 S[16];
+  // prologue: the committed state tile, then this block's normalised q / k, v and gates
+  float4 S[4];
   {
     const float* src = a.rec + slot * a.slot_stride + (size_t)hv * kGdnK * kGdnV + v0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) S[j] = *(const float4*)(src + (size_t)(16 * kg + j) * kGdnV);
+    for (int j = 0; j < 4; ++j) S[j] = *(const float4*)(src + (size_t)(k0 + j) * kGdnV);
   }
-
-  // b and a gates of every token: per-lane partial dot products over hidden, then a wave sum.
-  float bs[kGdnMaxM], as[kGdnMaxM];
-#pragma unroll
-  for (int t = 0; t < kGdnMaxM; ++t) bs[t] = as[t] = 0.f;
-  {
-    const uint16_t* wb = a.ba_w + (size_t)hv * a.hidden;
-    const uint16_t* wa = a.ba_w + (size_t)(a.HV + hv) * a.hidden;
-    for (int e = 8 * lane; e < a.hidden; e += 8 * 64) {
-      const uint4 ub = *(const uint4*)(wb + e), ua = *(const uint4*)(wa + e);
-      const uint32_t wbw[4] = {ub.x, ub.y, ub.z, ub.w}, waw[4] = {ua.x, ua.y, ua.z, ua.w};
-#pragma unroll
-      for (int t = 0; t < kGdnMaxM; ++t) {
-        if (t < M) {
-          const uint4 ux = *(const uint4*)(a.x + (size_t)t * a.hidden + e);
-          const uint32_t xw[4] = {ux.x, ux.y, ux.z, ux.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float x0 = bf16_bits_to_f32(xw[i] & 0xFFFFu), x1 = bf16_bits_to_f32(xw[i] >> 16);
-            bs[t] += x0 * bf16_bits_to_f32(wbw[i] & 0xFFFFu) + x1 * bf16_bits_to_f32(wbw[i] >> 16);
-            as[t] += x0 * bf16_bits_to_f32(waw[i] & 0xFFFFu) + x1 * bf16_bits_to_f32(waw[i] >> 16);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < kGdnMaxM; ++t) {
-      bs[t] = bf16r(wave_sum_f(bs[t]));
-      as[t] = bf16r(wave_sum_f(as[t]));
-    }
+  for (int e = tid; e < M * kGdnK; e += kGdnThreads) {
+    const int t = e / kGdnK, c = e % kGdnK;
+    cq[t][c] = a.qk[(size_t)t * 2 * QK + ih * kGdnK + c];
+    ck[t][c] = a.qk[(size_t)t * 2 * QK + QK + ih * kGdnK + c];
   }
-
-  // Causal conv + silu of this workgroup's 288 channels for all M tokens, into LDS. The ring
-  // column of position p is p % R; positions pos..pos+M-1 are this step's qkvz rows. The q/k
-  // channels of a key head are shared by HV / H value heads and four column blocks: only the
-  // first of them writes those ring columns (identical values; one writer keeps it race-free).
-  const bool qk_owner = (hv % (a.HV / a.H)) == 0 && vb == 0;
-  for (int idx = lane; idx < 2 * kGdnK + kGdnBV; idx += 64) {
-    int ch;
-    float* dst;
-    bool own;
-    if (idx < kGdnK) {
-      ch = ih * kGdnK + idx;
-      dst = &cq[0][idx];
-      own = qk_owner;
-    } else if (idx < 2 * kGdnK) {
-      ch = QK + ih * kGdnK + (idx - kGdnK);
-      dst = &ck[0][idx - kGdnK];
-      own = qk_owner;
-    } else {
-      ch = 2 * QK + hv * kGdnV + vb * kGdnBV + (idx - 2 * kGdnK);
-      dst = &cv[0][idx - 2 * kGdnK];
-      own = true;
-    }
-    const int stride = idx < 2 * kGdnK ? kGdnK : kGdnBV;  // LDS row pitch of dst
-    const uint2 wu = *(const uint2*)(a.conv_w + (size_t)ch * 4);
-    const float w0 = bf16_bits_to_f32(wu.x & 0xFFFFu), w1 = bf16_bits_to_f32(wu.x >> 16);
-    const float w2 = bf16_bits_to_f32(wu.y & 0xFFFFu), w3 = bf16_bits_to_f32(wu.y >> 16);
-    float win[kGdnMaxM + 3];
-    const uint16_t* rrow = a.ring + (size_t)ch * a.R;
-#pragma unroll
-    for (int j = 0; j < 3; ++j) win[j] = bf16_bits_to_f32(rrow[(int)((pos + j - 3 + 4 * (int64_t)a.R) % a.R)]);
-#pragma unroll
-    for (int t = 0; t < kGdnMaxM; ++t) win[t + 3] = t < M ? bf16_bits_to_f32(a.qkvz[(size_t)t * a.ld + ch]) : 0.f;
-#pragma unroll
-    for (int t = 0; t < kGdnMaxM; ++t) {
-      if (t < M) {
-        float yv = win[t] * w0;
-        yv = yv + win[t + 1] * w1;
-        yv = yv + win[t + 2] * w2;
-        yv = yv + win[t + 3] * w3;
-        yv = bf16r(yv);
-        dst[t * stride] = bf16r(yv / (1.f + expf(-yv)));
-      }
-    }
-    if (own) {
-      uint16_t* wrow = a.ring + (size_t)ch * a.R;
-      for (int t = 0; t < M; ++t) wrow[(int)((pos + t) % a.R)] = a.qkvz[(size_t)t * a.ld + ch];
-    }
+  for (int e = tid; e < M * kGdnBV; e += kGdnThreads) {
+    const int t = e / kGdnBV, c = e % kGdnBV;
+    cv[t][c] = bf16_bits_to_f32(a.vconv[(size_t)t * VAL + hv * kGdnV + vb * kGdnBV + c]);
+  }
+  if (tid < M) {
+    const float b = a.gates[(size_t)tid * 2 * a.HV + hv];
+    const float av = a.gates[(size_t)tid * 2 * a.HV + a.HV + hv];
+    beta_s[tid] = bf16r(1.f / (1.f + expf(-b)));
+    decay_s[tid] = expf(a.A[hv] * softplus_f(av + a.dt_bias[hv]));
   }
   __syncthreads();
 
-  const float Ah = a.A[hv], dtb = a.dt_bias[hv];
+  // the recurrence. With kv_t = sum_k S_{t-1}[k] k_t[k] (S before token t's decay):
+  //   dv = beta_t (v_t - e^{g_t} kv_t),  S_t = S_{t-1} e^{g_t} + k_t dv^T,  o_t = q_t^T S_t,
+  // and kv_{t+1} is summed together with o_t, so each token costs one cross-wave exchange.
+  // Sums over k: a lane's 4 rows, the wave's 8 row groups (lane ^ 8, ^ 16, ^ 32), the 4 waves.
+  auto ksum = [](float v) { return sum_x32(sum_x16(sum_x8(v))); };
+  auto wsum = [&](float4 p, int buf) {  // every lane of every wave must call it
+    p = make_float4(ksum(p.x), ksum(p.y), ksum(p.z), ksum(p.w));
+    if (kg == 0) red[buf][wave][vq] = p;
+    __syncthreads();
+    float4 r = red[buf][0][vq];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float4 u = red[buf][w][vq];
+      r.x += u.x;
+      r.y += u.y;
+      r.z += u.z;
+      r.w += u.w;
+    }
+    return r;
+  };
+  float4 kv;
+  {
+    float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float kk = ck[0][k0 + j];
+      p.x += S[j].x * kk;
+      p.y += S[j].y * kk;
+      p.z += S[j].z * kk;
+      p.w += S[j].w * kk;
+    }
+    kv = wsum(p, 0);
+  }
   float* const obase = a.o_ws + (size_t)hv * kGdnV + v0;
   for (int t = 0; t < M; ++t) {
-    // L2 norms of this token's q and k (all 128 channels), then this lane's 16 rows of each
-    float sq = cq[t][lane] * cq[t][lane] + cq[t][lane + 64] * cq[t][lane + 64];
-    float sk = ck[t][lane] * ck[t][lane] + ck[t][lane + 64] * ck[t][lane + 64];
-    const float nq = sqrtf(wave_sum_f(sq) + 1e-6f), nk = sqrtf(wave_sum_f(sk) + 1e-6f);
-    float qk[16], kk[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      qk[j] = cq[t][16 * kg + j] / nq * a.scale;
-      kk[j] = ck[t][16 * kg + j] / nk;
-    }
-    const float beta = bf16r(1.f / (1.f + expf(-bs[t])));
-    const float eg = expf(Ah * softplus_f(as[t] + dtb));
-    // decay, then the delta-rule correction along k
-    float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      S[j].x *= eg;
-      S[j].y *= eg;
-      S[j].z *= eg;
-      S[j].w *= eg;
-      kv.x += S[j].x * kk[j];
-      kv.y += S[j].y * kk[j];
-      kv.z += S[j].z * kk[j];
-      kv.w += S[j].w * kk[j];
-    }
-    kv.x = kg_sum(kv.x);
-    kv.y = kg_sum(kv.y);
-    kv.z = kg_sum(kv.z);
-    kv.w = kg_sum(kv.w);
-    const float* vt = &cv[t][4 * vq];
+    const float beta = beta_s[t], eg = decay_s[t];
+    const float* vt = &cv[t][c0];
     float4 dv;
-    dv.x = beta * (vt[0] - kv.x);
-    dv.y = beta * (vt[1] - kv.y);
-    dv.z = beta * (vt[2] - kv.z);
-    dv.w = beta * (vt[3] - kv.w);
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    dv.x = beta * (vt[0] - eg * kv.x);
+    dv.y = beta * (vt[1] - eg * kv.y);
+    dv.z = beta * (vt[2] - eg * kv.z);
+    dv.w = beta * (vt[3] - eg * kv.w);
+    const bool more = t + 1 < M;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f), nx = o;
     float* dst = a.rec + (size_t)t * a.slot_stride + (size_t)hv * kGdnK * kGdnV + v0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      S[j].x += kk[j] * dv.x;
-      S[j].y += kk[j] * dv.y;
-      S[j].z += kk[j] * dv.z;
-      S[j].w += kk[j] * dv.w;
-      *(float4*)(dst + (size_t)(16 * kg + j) * kGdnV) = S[j];
-      o.x += S[j].x * qk[j];
-      o.y += S[j].y * qk[j];
-      o.z += S[j].z * qk[j];
-      o.w += S[j].w * qk[j];
+    for (int j = 0; j < 4; ++j) {
+      const float kk = ck[t][k0 + j], qq = cq[t][k0 + j], kn = more ? ck[t + 1][k0 + j] : 0.f;
+      S[j].x = S[j].x * eg + kk * dv.x;
+      S[j].y = S[j].y * eg + kk * dv.y;
+      S[j].z = S[j].z * eg + kk * dv.z;
+      S[j].w = S[j].w * eg + kk * dv.w;
+      *(float4*)(dst + (size_t)(k0 + j) * kGdnV) = S[j];
+      o.x += S[j].x * qq;
+      o.y += S[j].y * qq;
+      o.z += S[j].z * qq;
+      o.w += S[j].w * qq;
+      nx.x += S[j].x * kn;
+      nx.y += S[j].y * kn;
+      nx.z += S[j].z * kn;
+      nx.w += S[j].w * kn;
     }
-    o.x = kg_sum(o.x);
-    o.y = kg_sum(o.y);
-    o.z = kg_sum(o.z);
-    o.w = kg_sum(o.w);
+    // both sums in one exchange: buffer (t + 1) % 2 alternates so the next token's writes never
+    // race this token's reads (the barrier inside wsum separates them)
+    o = make_float4(ksum(o.x), ksum(o.y), ksum(o.z), ksum(o.w));
+    nx = make_float4(ksum(nx.x), ksum(nx.y), ksum(nx.z), ksum(nx.w));
+    const int buf = (t + 1) & 1;
     if (kg == 0) {
+      red[buf][wave][vq] = o;
+      red_n[buf][wave][vq] = nx;
+    }
+    __syncthreads();
+    float4 ro = red[buf][0][vq], rn = red_n[buf][0][vq];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float4 u = red[buf][w][vq], q2 = red_n[buf][w][vq];
+      ro.x += u.x;
+      ro.y += u.y;
+      ro.z += u.z;
+      ro.w += u.w;
+      rn.x += q2.x;
+      rn.y += q2.y;
+      rn.z += q2.z;
+      rn.w += q2.w;
+    }
+    kv = rn;
+    if (wave == 0 && kg == 0) {
       float* op = obase + (size_t)t * VAL;
-      ws_st(op + 0, bf16r(o.x));
-      ws_st(op + 1, bf16r(o.y));
-      ws_st(op + 2, bf16r(o.z));
-      ws_st(op + 3, bf16r(o.w));
+      ws_st(op + 0, bf16r(ro.x));
+      ws_st(op + 1, bf16r(ro.y));
+      ws_st(op + 2, bf16r(ro.z));
+      ws_st(op + 3, bf16r(ro.w));
     }
   }
 
   // The last of the head's column blocks applies the gated norm to all V columns, every token.
+  // Its z and gain loads are issued before the arrival count.
+  const int Z = 2 * QK + VAL;
+  uint32_t zb[2][2];
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 4 * u;
+    const uint16_t* zr = a.qkvz + (size_t)t * a.ld + Z + (size_t)hv * kGdnV;
+    zb[u][0] = t < M ? zr[lane] : 0u;
+    zb[u][1] = t < M ? zr[lane + 64] : 0u;
+  }
+  const float nw0 = bf16_bits_to_f32(a.norm_w[lane]), nw1 = bf16_bits_to_f32(a.norm_w[lane + 64]);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (lane == 0) {
+  if (tid == 0) {
     int* c = a.cnt + hv * 32;
     const int old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = old == kGdnNVB - 1;
@@ -253,20 +338,19 @@ __global__ __launch_bounds__(64) void gdn_step_kernel(GdnArgs a) {
   }
   __syncthreads();
   if (!last) return;
-  const int Z = 2 * QK + VAL;
-  for (int t = 0; t < M; ++t) {
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 4 * u;
+    if (t >= M) break;
     const float* op = a.o_ws + (size_t)t * VAL + (size_t)hv * kGdnV;
     const float o0 = ws_ld(op + lane), o1 = ws_ld(op + lane + 64);
-    const float var = wave_sum_f(o0 * o0 + o1 * o1) / (float)kGdnV;
+    const float var = sum_wave(o0 * o0 + o1 * o1) / (float)kGdnV;
     const float r = 1.f / sqrtf(var + a.eps);
-    const uint16_t* zr = a.qkvz + (size_t)t * a.ld + Z + (size_t)hv * kGdnV;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int v = lane + 64 * h;
       const float ob = h ? o1 : o0;
-      const float n = bf16r(bf16r(ob * r) * bf16_bits_to_f32(a.norm_w[v]));
-      const float z = bf16_bits_to_f32(zr[v]);
-      a.y[(size_t)t * VAL + (size_t)hv * kGdnV + v] = f32_to_bf16_bits(n * (z / (1.f + expf(-z))));
+      const float n = bf16r(bf16r(ob * r) * (h ? nw1 : nw0));
+      const float z = bf16_bits_to_f32(zb[u][h]);
+      a.y[(size_t)t * VAL + (size_t)hv * kGdnV + lane + 64 * h] = f32_to_bf16_bits(n * (z / (1.f + expf(-z))));
     }
   }
 }
@@ -277,9 +361,16 @@ using namespace tr;
 
 extern "C" {
 
-size_t tr_gdn_workspace_bytes(int M, int HV) {
-  if (M < 1 || M > kGdnMaxM || HV < 1) return 0;
-  return (size_t)HV * 32 * sizeof(int) + (size_t)M * HV * kGdnV * sizeof(float);
+// Workspace: HV arrival counters (one per 128-byte line), the head outputs [M, HV V] fp32,
+// normalised q | k [M, 2 H K] fp32, the v conv outputs [M, HV V] bf16 and the gates [M, 2 HV]
+// fp32, each 256-byte aligned.
+static size_t gdn_ws_part(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
+size_t tr_gdn_workspace_bytes(int M, int H, int HV) {
+  if (M < 1 || M > kGdnMaxM || H < 1 || HV < 1) return 0;
+  return gdn_ws_part((size_t)HV * 32 * sizeof(int)) + gdn_ws_part((size_t)M * HV * kGdnV * sizeof(float)) +
+         gdn_ws_part((size_t)M * 2 * H * kGdnK * sizeof(float)) + gdn_ws_part((size_t)M * HV * kGdnV * 2) +
+         gdn_ws_part((size_t)M * 2 * HV * sizeof(float));
 }
 
 int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void* ring, const void* conv_w,
@@ -287,14 +378,14 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
                 const void* norm_w, const int64_t* pos, void* y, void* workspace, size_t workspace_bytes, int M,
                 int H, int HV, int K, int V, int hidden, int R, float eps, void* stream) {
   if (M == 0) return TR_OK;
-  if (M < 0 || M > kGdnMaxM || K != kGdnK || V != kGdnV || H < 1 || HV < H || HV % H || hidden < 8 ||
-      hidden % 8 || R < M + 3)
+  if (M < 0 || M > kGdnMaxM || K != kGdnK || V != kGdnV || H < 1 || HV < H || HV % H || (2 * H * K) % kGdnThreads ||
+      hidden < 32 || hidden % 32 || R < M + 3)
     return TR_ERR_SHAPE;
   if (!qkvz || !x || !ba_w || !ring || !conv_w || !A || !dt_bias || !rec || !slot || !norm_w || !pos || !y ||
       !workspace)
     return TR_ERR_ARG;
   if (ld < 2 * H * K + 2 * HV * V || slot_stride < (long)HV * K * V) return TR_ERR_ARG;
-  if (workspace_bytes < tr_gdn_workspace_bytes(M, HV)) return TR_ERR_ARG;
+  if (workspace_bytes < tr_gdn_workspace_bytes(M, H, HV)) return TR_ERR_ARG;
   GdnArgs a;
   a.qkvz = (const uint16_t*)qkvz;
   a.x = (const uint16_t*)x;
@@ -308,8 +399,16 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
   a.pos = pos;
   a.norm_w = (const uint16_t*)norm_w;
   a.y = (uint16_t*)y;
-  a.cnt = (int*)workspace;
-  a.o_ws = (float*)((char*)workspace + (size_t)HV * 32 * sizeof(int));
+  char* w = (char*)workspace;
+  a.cnt = (int*)w;
+  w += gdn_ws_part((size_t)HV * 32 * sizeof(int));
+  a.o_ws = (float*)w;
+  w += gdn_ws_part((size_t)M * HV * kGdnV * sizeof(float));
+  a.qk = (float*)w;
+  w += gdn_ws_part((size_t)M * 2 * H * K * sizeof(float));
+  a.vconv = (uint16_t*)w;
+  w += gdn_ws_part((size_t)M * HV * V * 2);
+  a.gates = (float*)w;
   a.slot_stride = slot_stride;
   a.ld = ld;
   a.hidden = hidden;
@@ -319,7 +418,11 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
   a.R = R;
   a.eps = eps;
   a.scale = 1.f / sqrtf((float)K);
-  hipLaunchKernelGGL(gdn_step_kernel, dim3(HV * kGdnNVB), dim3(64), 0, (hipStream_t)stream, a);
+  const int C = 2 * H * K + HV * V;
+  hipLaunchKernelGGL(gdn_prep_kernel, dim3((C + kGdnThreads - 1) / kGdnThreads + 2 * HV), dim3(kGdnThreads), 0,
+                     (hipStream_t)stream, a);
+  if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
+  hipLaunchKernelGGL(gdn_step_kernel, dim3(HV * kGdnNVB), dim3(kGdnThreads), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 

@@ -47,4 +47,41 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
   return r;
 }
 
+// Cross-lane sums on the VALU (DPP and the gfx950 permlane swaps) instead of LDS-routed
+// ds_bpermute shuffles. Each returns, in every lane, the sum over the lanes of its group; the
+// two lanes of a pair add the same two values (a + b == b + a), so every lane of a group ends
+// with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// lanes l and l ^ 8 (row_ror:8 inside each 16-lane row)
+__device__ __forceinline__ float sum_x8(float v) { return v + dpp_mov<0x128>(v); }
+// lanes l and l ^ 16: v_permlane16_swap leaves (row 2i, row 2i) in one result and
+// (row 2i + 1, row 2i + 1) in the other
+__device__ __forceinline__ float sum_x16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// lanes l and l ^ 32
+__device__ __forceinline__ float sum_x32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// the 32 lanes of the same parity (l % 2): quad xor 2, row_ror 4, row_ror 8, row pairs, halves
+__device__ __forceinline__ float sum_parity(float v) {
+  v = v + dpp_mov<0x4E>(v);
+  v = v + dpp_mov<0x124>(v);
+  v = sum_x8(v);
+  return sum_x32(sum_x16(v));
+}
+// all 64 lanes: quad xor 1, quad xor 2, row_ror 4, row_ror 8, then the row pairs and halves
+__device__ __forceinline__ float sum_wave(float v) {
+  v = v + dpp_mov<0xB1>(v);
+  v = v + dpp_mov<0x4E>(v);
+  v = v + dpp_mov<0x124>(v);
+  v = sum_x8(v);
+  return sum_x32(sum_x16(v));
+}
+
 }  // namespace tr

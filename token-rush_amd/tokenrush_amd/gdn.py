@@ -41,12 +41,12 @@ class GDNConfig:
 _ws = {}
 
 
-def workspace(M: int, HV: int, device):
-    """Per-device workspace (arrival counters + the head outputs for the gated norm), zero-filled
-    once: every call leaves its counters at zero."""
-    need = int(_lib.lib().tr_gdn_workspace_bytes(M, HV))
+def workspace(M: int, H: int, HV: int, device):
+    """Per-device workspace (arrival counters, head outputs for the gated norm, conv outputs and
+    gates of the step), zero-filled once: every call leaves its counters at zero."""
+    need = int(_lib.lib().tr_gdn_workspace_bytes(M, H, HV))
     if need == 0:
-        raise RuntimeError(f"gdn workspace: unsupported M={M} or HV={HV}")
+        raise RuntimeError(f"gdn workspace: unsupported M={M}, H={H} or HV={HV}")
     key = torch.device(device).index or 0
     ws = _ws.get(key)
     if ws is None or ws.numel() < need:
@@ -80,7 +80,7 @@ def gdn_step_fused(qkvz, x, ba_w, ring, conv_w, A, dt_bias, rec, slot, norm_w, p
     if tuple(rec.shape[1:]) != (HV, K, V) or rec.stride()[1:] != (K * V, V, 1):
         raise RuntimeError("gdn_step_fused: rec must be [n_slots, HV, K, V] with contiguous [HV, K, V] slots")
     y = torch.empty(M, HV * V, device=qkvz.device, dtype=bf)
-    ws = workspace(M, HV, qkvz.device)
+    ws = workspace(M, H, HV, qkvz.device)
     ld = qkvz.stride(0) if M > 1 else qkvz.shape[1]
     rc = _lib.lib().tr_gdn_step(
         _lib.ptr(qkvz), ld, _lib.ptr(x), _lib.ptr(ba_w), _lib.ptr(ring), _lib.ptr(conv_w), _lib.ptr(A),

@@ -2,25 +2,31 @@
 capturable as a single hipGraph.
 
 The layer body follows Engine._body (reference tokenrush/model.py:211-260) with the verify-path
-pieces of this package:
+kernels of this package:
 
     per layer li:
       x, n = add_rmsnorm(x, h, ln1)          h: the previous layer's down partials [S, M, hidden]
-      GDN layer (li % 4 != 3):  u = in_qkvz(n)   [M, 16384]   (model.py:76, marlin.mul)
-      attention (li % 4 == 3):  u = qkv(n)       [M, 14336]   (model.py:121)
-      y = mixer(u)                            [M, 6144]   STAND-IN (see below)
-      h = out.partials(y)                     [S, M, hidden] fp32 (model.py:85, split-K partials)
+      GDN layer (li % 4 != 3) (model.py:76-80, fused path):
+        u = in_qkvz(n)                        [M, 16384]  q | k | v | z
+        y = gdn_step_fused(u, n, ...)         [M, 6144]   conv ring, gates, delta rule with
+                                                          snapshot slots, gated norm (one launch)
+        h = out.partials(y)                   [S, M, hidden] fp32 split-K partials
+      attention layer (li % 4 == 3) (model.py:115-121, fused path):
+        u = qkv(n)                            [M, 14336]  q | gate per head, k, v
+        q = attn_prep(u, ...)                 q/k norm + rope, k/v into the FP8 cache
+        y = attn_decode_fused(q, u, ...)      [M, 6144]   flash-decoding + output gate
+        h = o.partials(y)
       x, n = add_rmsnorm(x, h, ln2)
       a = silu_mul(gate_up(n))                [M, 17408]  (model.py:156-160), one fused launch
-      h = down.partials(a)                    [S, M, hidden] fp32
+      h = down.partials(a)
     _, n = add_rmsnorm(x, h, final_norm); logits = lm_head(n)   [M, 248320]
     greedy accept: n_accepted, tok, pos += n + 1, slot = n (model.py:302-312), in the lm_head
     GEMM's epilogue (one launch)
 
-Stand-ins: the GDN recurrence (fused.py:119-237) and attention (fused.py:247-470) are not part of
-this build; each mixer is replaced by silu(u[:, :6144]) * u[:, 6144:12288], one launch that reads
-the projection output and writes the [M, 6144] input of the output projection. Every GEMM, the
-partial consumers, lm_head and the accept are the real kernels. The embedding gather is replaced
+The decode state (tokenrush/state.py:14-43) lives on the device: the position and the committed
+recurrent-state slot (read by the mixers, written by the accept), the conv rings and the fp32
+recurrent state in 8 snapshot slots per GDN layer, and the FP8 KV cache with per-(head, position)
+scales per attention layer, preloaded with `live` random tokens. The embedding gather is replaced
 by the step's input buffer x0.
 """
 from dataclasses import dataclass
@@ -29,8 +35,14 @@ import torch
 
 from . import gfx950
 from .accept import AcceptState, lm_head_greedy
-from .fused import add_rmsnorm, silu_mul
+from .attn import AttnConfig, attn_decode_fused, attn_prep, rope_table
+from .attn import workspace as attn_workspace
+from .fused import add_rmsnorm
+from .gdn import RING, GDNConfig, gdn_step_fused
+from .gdn import workspace as gdn_workspace
 from .quant import QLinear
+
+MAX_M = 8          # verify rows per step (1 committed + 7 drafts); also the snapshot slots
 
 
 @dataclass
@@ -38,18 +50,57 @@ class StepConfig:
     n_layers: int = 64
     hidden: int = 5120
     mlp: int = 17408
-    gdn_in: int = 16384        # in_qkvz output
-    attn_qkv: int = 14336      # q, k, v (+ gate) output
-    mixer_out: int = 6144      # input of the output projection
     vocab: int = 248320
     eps: float = 1e-6
     attn_every: int = 4        # layer li is full attention when li % attn_every == attn_every - 1
+    # GDN geometry (tokenrush/config.py:17-21)
+    gdn_k_heads: int = 16
+    gdn_v_heads: int = 48
+    gdn_k_dim: int = 128
+    gdn_v_dim: int = 128
+    # attention geometry (config.py:12-16)
+    n_heads: int = 24
+    n_kv_heads: int = 4
+    head_dim: int = 256
+    rotary_dim: int = 64
+    rope_theta: float = 1e7
+    live: int = 8192           # tokens already in the KV cache when the step runs
+    headroom: int = 1024       # cache rows past `live` for the steps that follow
 
     def is_attention(self, li: int) -> bool:
         return li % self.attn_every == self.attn_every - 1
 
+    @property
+    def gdn(self) -> GDNConfig:
+        return GDNConfig(self.hidden, self.gdn_k_heads, self.gdn_v_heads, self.gdn_k_dim, self.gdn_v_dim)
 
-SMALL = StepConfig(n_layers=4, hidden=512, mlp=1024, gdn_in=2048, attn_qkv=1792, mixer_out=768, vocab=4096)
+    @property
+    def attn(self) -> AttnConfig:
+        return AttnConfig(self.n_heads, self.n_kv_heads, self.head_dim, self.rotary_dim, self.rope_theta, self.eps)
+
+    @property
+    def gdn_in(self) -> int:       # in_qkvz output: conv channels + z
+        return self.gdn.conv_dim + self.gdn.gdn_val_dim
+
+    @property
+    def attn_qkv(self) -> int:     # q | gate per head, k, v
+        return self.n_heads * 2 * self.head_dim + 2 * self.n_kv_heads * self.head_dim
+
+    @property
+    def gdn_out(self) -> int:
+        return self.gdn.gdn_val_dim
+
+    @property
+    def attn_out(self) -> int:
+        return self.n_heads * self.head_dim
+
+    @property
+    def maxlen(self) -> int:
+        return self.live + self.headroom
+
+
+SMALL = StepConfig(n_layers=4, hidden=512, mlp=1024, vocab=4096, gdn_k_heads=2, gdn_v_heads=4, n_heads=2,
+                   n_kv_heads=1, live=300, headroom=64)
 
 
 def _random_linear(N, K, gen, device, split_k=1, scale_dtype=torch.bfloat16, layout="rows"):
@@ -62,22 +113,81 @@ def _random_linear(N, K, gen, device, split_k=1, scale_dtype=torch.bfloat16, lay
     return lin
 
 
+def _bf16(shape, std, gen, device, mean=0.0):
+    return (torch.randn(*shape, device=device, generator=gen) * std + mean).to(torch.bfloat16)
+
+
 class Layer:
     def __init__(self, cfg: StepConfig, li: int, gen, device):
         H = cfg.hidden
         self.attention = cfg.is_attention(li)
-        n_in = cfg.attn_qkv if self.attention else cfg.gdn_in
-        self.proj = _random_linear(n_in, H, gen, device)
-        self.out = _random_linear(H, cfg.mixer_out, gen, device, split_k=4)      # weights.py:163-174
+        if self.attention:
+            self.proj = _random_linear(cfg.attn_qkv, H, gen, device)
+            self.out = _random_linear(H, cfg.attn_out, gen, device, split_k=4)       # weights.py:163-174
+            self.q_norm_w = _bf16((cfg.head_dim,), 0.5, gen, device)
+            self.k_norm_w = _bf16((cfg.head_dim,), 0.5, gen, device)
+        else:
+            g = cfg.gdn
+            self.proj = _random_linear(cfg.gdn_in, H, gen, device)
+            self.out = _random_linear(H, cfg.gdn_out, gen, device, split_k=4)
+            self.in_ba = _bf16((2 * g.gdn_v_heads, H), 0.02, gen, device)
+            self.conv_w = _bf16((g.conv_dim, 4), 0.3, gen, device)
+            self.A = -torch.exp(torch.randn(g.gdn_v_heads, device=device, generator=gen))
+            self.dt_bias = torch.randn(g.gdn_v_heads, device=device, generator=gen)
+            self.norm_w = _bf16((g.gdn_v_dim,), 0.5, gen, device, mean=1.0)
         self.gate_up = _random_linear(2 * cfg.mlp, H, gen, device, layout="gate_up")   # silu fused in its epilogue
         self.down = _random_linear(H, cfg.mlp, gen, device, split_k=4)
-        self.ln1 = (torch.randn(H, device=device, generator=gen) * 0.1).to(torch.bfloat16)
-        self.ln2 = (torch.randn(H, device=device, generator=gen) * 0.1).to(torch.bfloat16)
+        self.ln1 = _bf16((H,), 0.1, gen, device)
+        self.ln2 = _bf16((H,), 0.1, gen, device)
+
+    def weight_bytes(self) -> int:
+        n = self.proj.nbytes + self.out.nbytes + self.gate_up.nbytes + self.down.nbytes
+        if not self.attention:
+            n += (self.in_ba.numel() + self.conv_w.numel() + self.norm_w.numel()) * 2 + self.A.numel() * 8
+        return n
+
+
+class StepState:
+    """Decode state of the step (tokenrush/state.py:14-43) for the GDN and attention layers:
+    position and committed slot, conv rings, recurrent state in MAX_M snapshot slots, FP8 KV
+    cache with per-(head, position) scales; rows 0..live-1 of the cache hold random tokens."""
+
+    def __init__(self, cfg: StepConfig, n_gdn: int, n_attn: int, gen, device):
+        g = cfg.gdn
+        self.pos = torch.full((1,), cfg.live, dtype=torch.int64, device=device)
+        self.slot = torch.zeros(1, dtype=torch.int64, device=device)
+        self.ring = _bf16((n_gdn, g.conv_dim, RING), 1.0, gen, device)
+        self.rec = torch.randn(MAX_M, n_gdn, g.gdn_v_heads, g.gdn_k_dim, g.gdn_v_dim, device=device,
+                               generator=gen) * 0.05
+        HKV, D, L = cfg.n_kv_heads, cfg.head_dim, cfg.maxlen
+        self.k = torch.zeros(n_attn, HKV, L, D, dtype=torch.float8_e4m3fn, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.k_scale = torch.full((n_attn, HKV, L), 0.01, device=device)
+        self.v_scale = torch.full((n_attn, HKV, L), 0.01, device=device)
+        for a in range(n_attn):
+            self.k[a, :, :cfg.live] = (torch.randn(HKV, cfg.live, D, device=device, generator=gen) * 64).to(
+                torch.float8_e4m3fn)
+            self.v[a, :, :cfg.live] = (torch.randn(HKV, cfg.live, D, device=device, generator=gen) * 64).to(
+                torch.float8_e4m3fn)
+        self.cos, self.sin = rope_table(L, cfg.rotary_dim, cfg.rope_theta, device)
+
+    def tensors(self):
+        return [self.pos, self.slot, self.ring, self.rec, self.k, self.v, self.k_scale, self.v_scale]
+
+    def snapshot(self):
+        return [t.clone() for t in self.tensors()]
+
+    def restore(self, snap):
+        for t, s in zip(self.tensors(), snap):
+            t.copy_(s)
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self.tensors()[2:])
 
 
 class VerifyModel:
-    """Random-init weights of the config-5 hybrid (int4 g128, bf16 scale/min) and the verify step.
-    Weights are packed once at construction (QLinear packs them into the quad layout)."""
+    """Random-init weights and decode state of the config-5 hybrid (int4 g128 projections,
+    bf16 scale/min) and the verify step. Weights are packed once at construction."""
 
     def __init__(self, cfg: StepConfig = StepConfig(), device="cuda:0", seed: int = 0):
         self.cfg = cfg
@@ -85,41 +195,53 @@ class VerifyModel:
         gen = torch.Generator(device=self.device)
         gen.manual_seed(seed)
         self.layers = [Layer(cfg, li, gen, self.device) for li in range(cfg.n_layers)]
-        self.final_norm = (torch.randn(cfg.hidden, device=self.device, generator=gen) * 0.1).to(torch.bfloat16)
+        self.final_norm = _bf16((cfg.hidden,), 0.1, gen, self.device)
         self.lm_head = _random_linear(cfg.vocab, cfg.hidden, gen, self.device)
+        self.gdn_index, self.attn_index = {}, {}
+        for li, L in enumerate(self.layers):
+            d = self.attn_index if L.attention else self.gdn_index
+            d[li] = len(d)
+        self.state = StepState(cfg, len(self.gdn_index), len(self.attn_index), gen, self.device)
 
     def nbytes(self) -> int:
-        n = self.lm_head.nbytes
-        for L in self.layers:
-            n += L.proj.nbytes + L.out.nbytes + L.gate_up.nbytes + L.down.nbytes
-        return n
+        return self.lm_head.nbytes + sum(L.weight_bytes() for L in self.layers)
 
-    def mixer(self, u: torch.Tensor) -> torch.Tensor:
-        """Stand-in for the GDN / attention mixer: [M, n_in] -> [M, mixer_out]."""
-        F = self.cfg.mixer_out
-        return silu_mul(u[:, :2 * F])
+    def mixer(self, li: int, L: Layer, n: torch.Tensor, pos_t, slot_t) -> torch.Tensor:
+        """The layer's token mixer: [M, hidden] normed input -> [M, mixer out] (model.py:76-121)."""
+        cfg, st = self.cfg, self.state
+        u = L.proj(n)
+        if L.attention:
+            a = self.attn_index[li]
+            q = attn_prep(u, L.q_norm_w, L.k_norm_w, st.cos, st.sin, pos_t, st.k[a], st.v[a], cfg.attn,
+                          st.k_scale[a], st.v_scale[a])
+            return attn_decode_fused(q, u, st.k[a], st.v[a], pos_t, cfg.attn, st.k_scale[a], st.v_scale[a])
+        g = self.gdn_index[li]
+        return gdn_step_fused(u, n, L.in_ba, st.ring[g], L.conv_w, L.A, L.dt_bias, st.rec[:, g], slot_t, L.norm_w,
+                              pos_t, cfg.gdn, cfg.eps)
 
-    def hidden(self, x0: torch.Tensor) -> torch.Tensor:
+    def hidden(self, x0: torch.Tensor, pos_t=None, slot_t=None) -> torch.Tensor:
         """x0 [M, hidden] bf16 -> post-final-norm hidden [M, hidden] bf16 (model.py:252-254)."""
         cfg = self.cfg
+        pos_t = self.state.pos if pos_t is None else pos_t
+        slot_t = self.state.slot if slot_t is None else slot_t
         x, h = x0, None
-        for L in self.layers:
+        for li, L in enumerate(self.layers):
             x, n = add_rmsnorm(x, h, L.ln1, cfg.eps)
-            y = self.mixer(L.proj(n))
-            h = L.out.partials(y)
+            h = L.out.partials(self.mixer(li, L, n, pos_t, slot_t))
             x, n = add_rmsnorm(x, h, L.ln2, cfg.eps)
             h = L.down.partials(L.gate_up.silu_mul(n))
         _, n = add_rmsnorm(x, h, self.final_norm, cfg.eps)
         return n
 
     def body(self, x0: torch.Tensor) -> torch.Tensor:
-        """x0 [M, hidden] bf16 -> logits [M, vocab] bf16."""
+        """x0 [M, hidden] bf16 -> logits [M, vocab] bf16, at the state's position and slot."""
         return self.lm_head(self.hidden(x0))
 
     def step(self, x0: torch.Tensor, spec_toks: torch.Tensor, st: AcceptState) -> torch.Tensor:
-        """Body + lm_head with the greedy accept/commit in its epilogue (one launch). Returns the
-        logits, kept as the reference keeps them (model.py:300; graph-owned under capture)."""
-        return lm_head_greedy(self.lm_head, self.hidden(x0), spec_toks, st, keep_logits=True)
+        """Body at st.pos / st.slot + lm_head with the greedy accept/commit in its epilogue (one
+        launch), which advances st.pos by n + 1 and sets st.slot = n. Returns the logits, kept as
+        the reference keeps them (model.py:300; graph-owned under capture)."""
+        return lm_head_greedy(self.lm_head, self.hidden(x0, st.pos, st.slot), spec_toks, st, keep_logits=True)
 
 
 def prepare(model: VerifyModel, M: int):
@@ -129,3 +251,5 @@ def prepare(model: VerifyModel, M: int):
         for lin in (L.proj, L.gate_up):
             gfx950.workspaces(lin.shape[0], model.device, lin.shape[1], M)
     gfx950.workspaces(cfg.vocab, model.device, cfg.hidden, M)
+    gdn_workspace(M, cfg.gdn_k_heads, cfg.gdn_v_heads, model.device)
+    attn_workspace(M, cfg.n_heads, 32, model.device)
