@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import attn as o
-from tokenrush_amd.attn import AttnConfig, attn_decode_fused, attn_prep, rope_table
+from tokenrush_amd.attn import NSPLIT, AttnConfig, attn_decode_fused, attn_prep, rope_table
 
 pytestmark = pytest.mark.gpu
 CFG = AttnConfig()
@@ -88,7 +88,7 @@ def test_attn_decode_matches_oracle(dev, M, pos):
     out = attn_decode_fused(q, qkv, kc, vc, torch.tensor([pos], device=dev), CFG, ks, vs)
     torch.cuda.synchronize()
     ref = o.attn_decode(_np(q).reshape(M, HQ, D), _np(qkv), _codes(kc), _codes(vc), _np(ks), _np(vs), pos, HQ, HKV, D,
-                        nsplit=32)
+                        nsplit=NSPLIT)
     got = _np(out)
     assert np.isfinite(got).all()
     for t in range(M):

@@ -11,6 +11,7 @@ import torch
 from oracle import accept as oa
 from oracle import attn as oat
 from oracle import gdn as og
+from tokenrush_amd.attn import NSPLIT
 
 pytestmark = pytest.mark.gpu
 
@@ -55,7 +56,8 @@ def _ref_body(model, x0):
             q, kc[a], vc[a], ks[a], vs[a] = oat.attn_prep(npf(u), npf(L.q_norm_w), npf(L.k_norm_w), cos, sin, pos,
                                                           kc[a], vc[a], ks[a], vs[a], cfg.n_heads, cfg.n_kv_heads,
                                                           cfg.head_dim, cfg.rotary_dim, cfg.eps)
-            y = oat.attn_decode(q, npf(u), kc[a], vc[a], ks[a], vs[a], pos, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim)
+            y = oat.attn_decode(q, npf(u), kc[a], vc[a], ks[a], vs[a], pos, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                nsplit=NSPLIT)
         else:
             k = model.gdn_index[li]
             y, ring[k], rec_k = og.gdn_step(npf(u), npf(n), npf(L.in_ba), ring[k], npf(L.conv_w), npf(L.A),

@@ -36,13 +36,6 @@ constexpr int kMaxSplit = 256;  // key-range splits of one flash-decoding call
 
 // ------------------------------------------------------------------ fp8 e4m3fn (OCP) helpers
 
-// fp8 e4m3fn bits -> fp32 (exact). NaN (0x7F / 0xFF) is never produced by this path's writers.
-__device__ __forceinline__ float fp8_to_f32(uint32_t b) {
-  const uint32_t e = (b >> 3) & 0xF, m = b & 7;
-  const float mag = e == 0 ? (float)m * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
-  return (b & 0x80) ? -mag : mag;
-}
-
 // fp32 -> fp8 e4m3fn bits, round to nearest even; magnitudes past the largest finite value
 // (448) saturate to it (the writers keep |x| <= 448 up to rounding).
 __device__ __forceinline__ uint32_t f32_to_fp8(float x) {
@@ -63,6 +56,31 @@ __device__ __forceinline__ uint32_t f32_to_fp8(float x) {
 }
 
 __device__ __forceinline__ float bf16r_a(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+// Two fp32 -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pk_bf16(float x, float y) {
+  const bf16x2v r = {(__bf16)x, (__bf16)y};
+  return __builtin_bit_cast(uint32_t, r);
+}
+// fp8 e4m3fn bytes 0,1 (hi = false) or 2,3 (hi = true) of w -> fp32, exact (v_cvt_pk_f32_fp8).
+__device__ __forceinline__ f32x2v fp8x2_to_f32(uint32_t w, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true) : __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+}
+// Exact fp8 -> bf16 of two values: the fp32 images have zero low halves.
+__device__ __forceinline__ uint32_t fp8x2_to_bf16(uint32_t w, bool hi) {
+  const f32x2v f = fp8x2_to_f32(w, hi);
+  return (__float_as_uint(f.x) >> 16) | (__float_as_uint(f.y) & 0xFFFF0000u);
+}
+__device__ __forceinline__ float max_x16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 // ------------------------------------------------------------------ prep
 
@@ -256,24 +274,24 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
         uint32_t o[4];
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-          const uint32_t w = kw[2 * q4 + h / 2];
-          const uint32_t b0_ = (w >> (16 * (h & 1))) & 0xFF, b1_ = (w >> (16 * (h & 1) + 8)) & 0xFF;
-          o[h] = (uint32_t)f32_to_bf16_bits(fp8_to_f32(b0_) * sck) |
-                 ((uint32_t)f32_to_bf16_bits(fp8_to_f32(b1_) * sck) << 16);
+          const f32x2v f = fp8x2_to_f32(kw[2 * q4 + h / 2], h & 1);
+          o[h] = pk_bf16(f.x * sck, f.y * sck);
         }
         *(uint4*)(dst + 8 * q4) = make_uint4(o[0], o[1], o[2], o[3]);
       }
       if ((tid & 7) == 0) ksc[fk] = sck;
     }
     {
+      // 4 keys x 8 dims -> 8 rows of V^T (4 keys each): byte e of key i is pv[i] byte e
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
+        const int sh = 8 * (e & 3);
         uint32_t b[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) b[i] = ((e < 4 ? pv[i].x : pv[i].y) >> (8 * (e & 3))) & 0xFF;
+        for (int i = 0; i < 4; ++i) b[i] = ((e < 4 ? pv[i].x : pv[i].y) >> sh) & 0xFF;
         uint2 o;
-        o.x = (uint32_t)f32_to_bf16_bits(fp8_to_f32(b[0])) | ((uint32_t)f32_to_bf16_bits(fp8_to_f32(b[1])) << 16);
-        o.y = (uint32_t)f32_to_bf16_bits(fp8_to_f32(b[2])) | ((uint32_t)f32_to_bf16_bits(fp8_to_f32(b[3])) << 16);
+        o.x = fp8x2_to_bf16(b[0] | (b[1] << 8), false);
+        o.y = fp8x2_to_bf16(b[2] | (b[3] << 8), false);
         *(uint2*)(Vt + (fvd + e) * kVPitch + fv) = o;
       }
       if (tid < kAttnBlk) vsc[tid] = psv;
@@ -308,8 +326,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
         sc[4 * kt + r] = v;
         mx = fmaxf(mx, v);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max_x32(max_x16(mx));
     const float m_new = fmaxf(m_i, mx);
     const float m_safe = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = expf(m_i - m_safe);
@@ -320,10 +337,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
       const float p0 = expf(sc[i] - m_safe), p1 = expf(sc[i + 1] - m_safe);
       psum += p0 + p1;
       const int k0 = 16 * (i / 4) + 4 * (lane >> 4) + (i & 3);
-      pb[i / 2] = (uint32_t)f32_to_bf16_bits(p0 * vsc[k0]) | ((uint32_t)f32_to_bf16_bits(p1 * vsc[k0 + 1]) << 16);
+      pb[i / 2] = pk_bf16(p0 * vsc[k0], p1 * vsc[k0 + 1]);
     }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
+    psum = sum_x32(sum_x16(psum));
     l_i = l_i * alpha + psum;
     m_i = m_new;
     // O^T += V^T P^T: k-index 8 (l / 16) + i <-> key 4 (l / 16) + i (i < 4), 16 + 4 (l / 16) + i - 4

@@ -14,7 +14,8 @@ import torch
 
 from . import _lib
 
-NSPLIT = 32        # key-range splits of the flash-decoding kernel (the reference's default)
+NSPLIT = 64        # key-range splits of the flash-decoding kernel: 256 workgroups at 4 kv heads
+                   # (the reference uses 32 on a 170-SM part; measured fastest here)
 
 
 @dataclass(frozen=True)

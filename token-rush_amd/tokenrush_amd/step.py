@@ -36,6 +36,7 @@ import torch
 from . import gfx950
 from .accept import AcceptState, lm_head_greedy
 from .attn import AttnConfig, attn_decode_fused, attn_prep, rope_table
+from .attn import NSPLIT as ATTN_NSPLIT
 from .attn import workspace as attn_workspace
 from .fused import add_rmsnorm
 from .gdn import RING, GDNConfig, gdn_step_fused
@@ -252,4 +253,4 @@ def prepare(model: VerifyModel, M: int):
             gfx950.workspaces(lin.shape[0], model.device, lin.shape[1], M)
     gfx950.workspaces(cfg.vocab, model.device, cfg.hidden, M)
     gdn_workspace(M, cfg.gdn_k_heads, cfg.gdn_v_heads, model.device)
-    attn_workspace(M, cfg.n_heads, 32, model.device)
+    attn_workspace(M, cfg.n_heads, ATTN_NSPLIT, model.device)
