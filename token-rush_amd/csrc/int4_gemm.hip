@@ -171,11 +171,12 @@ struct GemmArgs {
   int* am_cnt;            // arrival counter, zero between calls
   const int64_t* spec;    // [M] committed token + drafts, or null (argmax only)
   AcceptOut o;            // o.pred [M] always; the rest when spec != null
+  int xstage_off;         // byte offset of the activation staging area in dynamic LDS (M <= 8)
 };
 
 // One accumulator tile element: (mt, lane, r) -> output row m = 16 mt + 4 (lane / 16) + r,
 // column n = 16 strip + lane % 16.
-template <int MT, int GW, bool F16S>
+template <int MT, int GW, bool F16S, bool XDMA>
 __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   extern __shared__ float red[];  // [2][RB][W][MT][64][4]
   __shared__ uint64_t rowbest[32];  // fused argmax: best key per output row
@@ -216,10 +217,35 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // parameters of row lane % 16, groups gbase % 4 .. + GW - 1, relative to the strip offset
   const int sm_voff = kSmOff + 16 * (lane & 15) + 4 * (gbase % kQuad) - (gbase % kQuad) * kCodeBytes;
 
-  // Activations of this wave's K block, in registers for the whole strip loop. Padding groups
-  // (g >= G) read group G - 1: finite values that meet zero scale and min.
+  // Activations of this wave's K block, in registers for the whole strip loop, in the MFMA
+  // A-operand layout (lane l: row l % 16 of its row tile, k = 32 j + 8 (l / 16) .. + 7 of MFMA j).
+  // Padding groups (g >= G) read group G - 1: finite values that meet zero scale and min.
   uint4 xa[GW][MT][4];
-  {
+  if constexpr (XDMA) {
+    // M <= 8: load the rows coalesced -- a 64-lane load covers four whole 256-byte row segments
+    // of a group -- straight into this wave's LDS staging area (buffer_load ... lds, no VGPRs),
+    // then read them back in the operand layout. In the operand layout itself consecutive lanes
+    // would read different rows, each lane a separate cache access, which took 3-6 us for these
+    // 8 KB per wave. Chunk k of row r sits in 16-byte slot k ^ r of the row, so the 16 rows read
+    // by one operand load fall in different LDS banks. Rows >= M read zeros (out-of-range
+    // offsets: no memory access) and are never used.
+    static_assert(MT == 1, "activation staging covers one row tile");
+    char* stage = (char*)red + a.xstage_off + wave * (GW * 2048);
+    const int xbytes = a.M * a.K * 2;
+    const auto xrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, xbytes, 0x00020000);
+    const int lr = lane >> 4, lk = lane & 15;
+#pragma unroll
+    for (int gw = 0; gw < GW; ++gw) {
+      const int g = min(gbase + gw, G - 1);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int r = 4 * c + lr;
+        const int off = r < a.M ? (r * a.K + g * kGroup) * 2 + ((lk ^ r) & 15) * 16 : xbytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(stage + gw * 2048 + c * 1024),
+                                                 16, off, 0, 0, 0);
+      }
+    }
+  } else {
 #pragma unroll
     for (int gw = 0; gw < GW; ++gw) {
       const int g = min(gbase + gw, G - 1);
@@ -232,13 +258,25 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
       }
     }
   }
-  // Two strips in flight. Issued after the activation loads: vmcnt counts loads in issue
-  // order, so the selector MFMAs below wait only for the (L2-resident) activations and each
-  // tile_mac only for its own strip's loads.
+  // Two strips in flight, issued after the activation loads (vmcnt counts loads in issue order,
+  // so waiting for the activations leaves the strips in flight). Waves without a K block issue
+  // out-of-range loads: no memory access, the same count.
   Strip<GW> buf[2];
-  if (active) {
-    load_strip<GW>(buf[0], rsrc, strip_off(r0), lane_off, sm_voff);
-    load_strip<GW>(buf[1], rsrc, strip_off(r0 + 1), lane_off, sm_voff);
+  load_strip<GW>(buf[0], rsrc, active ? strip_off(r0) : oob, lane_off, sm_voff);
+  load_strip<GW>(buf[1], rsrc, active ? strip_off(r0 + 1) : oob, lane_off, sm_voff);
+  if constexpr (XDMA) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (GW + 1)) : "memory");  // the staging loads have landed
+    const char* stage = (const char*)red + a.xstage_off + wave * (GW * 2048);
+    const int i = lane & 15;
+#pragma unroll
+    for (int gw = 0; gw < GW; ++gw) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = 4 * j + (lane >> 4);
+        const uint4 v = *(const uint4*)(stage + gw * 2048 + (i & 7) * 256 + ((k ^ i) & 15) * 16);
+        xa[gw][0][j] = i < a.M ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
   }
 
   // Xa[mt] = sum of x over group gbase + lane / 16 for row 16 mt + lane % 16 (the A operand of
@@ -537,7 +575,8 @@ bool shape_ok(int N, int K) {
   return N > 0 && K > 0 && N % 16 == 0 && K % kGroup == 0 && packed_bytes(N, K) < ((size_t)1 << 31);
 }
 constexpr int kWavesPerCU = 12;    // occupancy of the GEMM kernel (about 150 VGPRs per lane)
-constexpr size_t kLdsBudget = 64 * 1024;  // dynamic LDS of one workgroup (the default limit)
+constexpr size_t kLdsBudget = 64 * 1024;  // LDS of the reduction ring
+constexpr size_t kLdsMax = 152 * 1024;    // dynamic LDS of one workgroup: gfx950's 160 KB less the kernel's static LDS
 
 struct Plan {
   int GW, S, W, R, grid_n;
@@ -572,20 +611,35 @@ bool make_plan(int N, int K, int M, int S_req, int R_req, Plan* p) {
   return true;
 }
 
-template <int MT, int GW, bool F16S>
+template <int MT, int GW, bool F16S, bool XDMA>
 hipError_t launch_t(GemmArgs a, const Plan& p, hipStream_t stream) {
   const dim3 grid(p.grid_n * p.S), block(64 * p.W);
   const size_t per_strip = (size_t)p.W * MT * 256 * sizeof(float);
   int rb = (int)(kLdsBudget / (2 * per_strip));
   a.RB = rb < 1 ? 1 : (rb > 4 ? 4 : rb);
-  hipLaunchKernelGGL((int4_gemm_kernel<MT, GW, F16S>), grid, block, 2 * a.RB * per_strip, stream, a);
+  const size_t ring = 2 * a.RB * per_strip;
+  a.xstage_off = (int)ring;
+  const size_t lds = XDMA ? ring + (size_t)p.W * GW * 2048 : ring;
+  if (XDMA) {
+    // staging + ring exceed the default 64 KB of dynamic LDS: raise this kernel's limit once
+    static bool raised = false;
+    if (!raised) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&int4_gemm_kernel<MT, GW, F16S, XDMA>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+      if (e != hipSuccess) return e;
+      raised = true;
+    }
+    if (lds > kLdsMax) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((int4_gemm_kernel<MT, GW, F16S, XDMA>), grid, block, lds, stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch(const GemmArgs& a, const Plan& p, int scale_dtype, hipStream_t stream) {  // NOLINT
   const bool f16 = scale_dtype == 1;
-  if (a.M > 16) return f16 ? launch_t<2, 2, true>(a, p, stream) : launch_t<2, 2, false>(a, p, stream);
-  return f16 ? launch_t<1, 4, true>(a, p, stream) : launch_t<1, 4, false>(a, p, stream);
+  if (a.M > 16) return f16 ? launch_t<2, 2, true, false>(a, p, stream) : launch_t<2, 2, false, false>(a, p, stream);
+  if (a.M <= 8) return f16 ? launch_t<1, 4, true, true>(a, p, stream) : launch_t<1, 4, false, true>(a, p, stream);
+  return f16 ? launch_t<1, 4, true, false>(a, p, stream) : launch_t<1, 4, false, false>(a, p, stream);
 }
 
 }  // namespace
