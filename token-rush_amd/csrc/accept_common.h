@@ -61,7 +61,7 @@ struct AcceptOut {
 
 // Engine._verify_step (tokenrush/model.py:302-312): match = pred[:K] == spec[1:M],
 // n = leading matches, tok = pred[n], pos += n + 1, slot = n.
-static __device__ void finish_chain(const int64_t* pred, const int64_t* spec, int M, const AcceptOut& o) {
+static __device__ __forceinline__ void finish_chain(const int64_t* pred, const int64_t* spec, int M, const AcceptOut& o) {
   int n = 0;
   while (n < M - 1 && pred[n] == spec[n + 1]) ++n;
   const int64_t base = *o.pos;

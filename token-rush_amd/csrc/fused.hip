@@ -23,36 +23,21 @@ enum { H_NONE = 0, H_BF16 = 1, H_PARTIALS = 2 };
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
+// Sum over the workgroup: each wave's lanes by sum_wave, then the waves in index order (the same
+// order in every thread, and the order of the GEMM's norm epilogue).
 __device__ __forceinline__ float block_sum(float v, float* sh) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  v = sum_wave(v);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (lane == 0) sh[wave] = v;
   __syncthreads();
   float t = 0.f;
   const int nw = blockDim.x >> 6;
-  for (int w = 0; w < nw; ++w) t += sh[w];  // same order in every thread
+  for (int w = 0; w < nw; ++w) t += sh[w];
   return t;
 }
 
-__device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = bf16_bits_to_f32(w[i] & 0xFFFFu);
-    f[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
-  }
-}
-
-__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f32_to_bf16_bits(f[2 * i]) | ((uint32_t)f32_to_bf16_bits(f[2 * i + 1]) << 16);
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
-// One workgroup per row, 8 consecutive elements per thread, every load of the row (x and all S
-// partial slots) issued before any arithmetic.
+// One workgroup per row, 8 consecutive elements per thread, every load of the row (x, all S
+// partial slots and the gain) issued before any arithmetic.
 template <int HM, int S>
 __global__ __launch_bounds__(kMaxRowThreads) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, const void* h,
                                                                      const uint16_t* __restrict__ w, uint16_t* xo,
@@ -64,12 +49,13 @@ __global__ __launch_bounds__(kMaxRowThreads) void add_rmsnorm_kernel(const uint1
   const bool on = i0 < N;
   const size_t row = (size_t)t * N + i0;
   float v[kRowVec];
-  uint4 xv = make_uint4(0, 0, 0, 0), hv = xv;
+  uint4 xv = make_uint4(0, 0, 0, 0), hv = xv, wv = xv;
   float4 part[S > 0 ? S : 1][2];
 #pragma unroll
   for (int s = 0; s < (S > 0 ? S : 1); ++s) part[s][0] = part[s][1] = make_float4(0.f, 0.f, 0.f, 0.f);
   if (on) {
     xv = *(const uint4*)(x + row);
+    wv = *(const uint4*)(w + i0);
     if (HM == H_BF16) hv = *(const uint4*)((const uint16_t*)h + row);
     if (HM == H_PARTIALS) {
 #pragma unroll
@@ -91,24 +77,19 @@ __global__ __launch_bounds__(kMaxRowThreads) void add_rmsnorm_kernel(const uint1
         float acc = e < 4 ? part[0][0][e] : part[0][1][e - 4];
 #pragma unroll
         for (int s = 1; s < S; ++s) acc += e < 4 ? part[s][0][e] : part[s][1][e - 4];  // slot order
-        hf[e] = bf16_bits_to_f32(f32_to_bf16_bits(acc));
+        hf[e] = acc;
       }
     }
 #pragma unroll
-    for (int e = 0; e < kRowVec; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] + hf[e]));  // bf16 residual
+    for (int e = 0; e < kRowVec; ++e) v[e] = resid_add(v[e], hf[e]);  // bf16(x + bf16(h))
     if (on) *(uint4*)(xo + row) = pack8(v);
   }
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < kRowVec; ++e) ss = fmaf(v[e], v[e], ss);
-  const float r = 1.0f / sqrtf(block_sum(ss, sh) / (float)N + eps);
+  const float r = rms_inv(block_sum(ssq8(v), sh), N, eps);
   if (!on) return;
   float wf[kRowVec], out[kRowVec];
-  unpack8(*(const uint4*)(w + i0), wf);
+  unpack8(wv, wf);
 #pragma unroll
-  for (int e = 0; e < kRowVec; ++e)
-    out[e] = plain ? wf[e] * bf16_bits_to_f32(f32_to_bf16_bits(v[e] * r))  // Qwen3: cast, then weight * x
-                   : v[e] * r * (1.0f + wf[e]);                              // Qwen3.5: gain is 1 + weight
+  for (int e = 0; e < kRowVec; ++e) out[e] = rms_apply(v[e], r, wf[e], plain);  // Qwen3.5 (1 + w) or Qwen3 plain
   *(uint4*)(y + row) = pack8(out);
 }
 

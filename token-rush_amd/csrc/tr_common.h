@@ -39,6 +39,46 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
 // GEMM epilogue and the stand-alone kernel, so the two paths agree bit for bit.
 __device__ __forceinline__ float silu_mul_f32(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
+// 8 bf16 (one 16-byte load) <-> fp32.
+__device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_bits_to_f32(w[i] & 0xFFFFu);
+    f[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+  }
+}
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f32_to_bf16_bits(f[2 * i]) | ((uint32_t)f32_to_bf16_bits(f[2 * i + 1]) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Pieces of the residual RMSNorm (tokenrush/fused.py:23-60) shared by add_rmsnorm_kernel and the
+// GEMM's norm epilogue, so that the two paths give the same bits whatever each file's
+// contraction flags: the residual bf16(x + bf16(h)), the inverse RMS from a row's sum of
+// squares, and the gain ((1 + w), or the plain w * bf16(x * r)).
+__device__ __forceinline__ float resid_add(float x, float h) {
+#pragma clang fp contract(off)
+  return bf16_bits_to_f32(f32_to_bf16_bits(x + bf16_bits_to_f32(f32_to_bf16_bits(h))));
+}
+__device__ __forceinline__ float rms_inv(float ss, int N, float eps) {
+#pragma clang fp contract(off)
+  return 1.0f / sqrtf(ss / (float)N + eps);
+}
+__device__ __forceinline__ float rms_apply(float v, float r, float w, int plain) {
+#pragma clang fp contract(off)
+  return plain ? w * bf16_bits_to_f32(f32_to_bf16_bits(v * r)) : v * r * (1.0f + w);
+}
+// Sum of squares of 8 consecutive elements, in element order.
+__device__ __forceinline__ float ssq8(const float (&v)[8]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+  return ss;
+}
+
 // A value the compiler must keep in a VGPR: lets v_and_or_b32 take (VGPR, SGPR, VGPR)
 // operands, since a gfx9 VOP3 instruction reads at most one scalar/literal.
 __device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
