@@ -148,3 +148,28 @@ def test_step_accept_and_graph_replay(small_model):
         assert torch.equal(st.n_accepted, eager[1]) and torch.equal(st.tok, eager[2]), rep
         assert torch.equal(st.slot, eager[3]) and torch.equal(st.tokens, eager[4]) and torch.equal(st.commit, eager[5])
         assert int(st.pos) == want["pos"]
+
+
+def test_checkpoint_round_trip(small_model, tmp_path):
+    """The model written in the packed checkpoint format (weights.py:60-102) and loaded back
+    (weights.py:238-254): same engine-packed nibbles for every matrix, same small tensors, and the
+    same step output bit for bit from the same decode state."""
+    from tokenrush_amd.step import VerifyModel
+    print("checkpoint round trip", flush=True)
+    m = small_model
+    info = m.save_checkpoint(str(tmp_path))
+    assert "lm_head.weight" in info["quantized"] and "layers.0.mlp.gate_proj.weight" in info["quantized"]
+    m2 = VerifyModel.from_checkpoint(str(tmp_path), device="cuda:0", live=m.cfg.live, headroom=m.cfg.headroom)
+    for L, L2 in zip(m.layers, m2.layers):
+        assert L.attention == L2.attention
+        for a in ("proj", "out", "gate_up", "down"):
+            for t, t2 in zip(getattr(L, a).nibbles(), getattr(L2, a).nibbles()):
+                assert torch.equal(t, t2), a
+        small = ("q_norm_w", "k_norm_w") if L.attention else ("in_ba", "conv_w", "A", "dt_bias", "norm_w")
+        for a in small + ("ln1", "ln2"):
+            assert torch.equal(getattr(L, a), getattr(L2, a)), a
+    m2.state.restore(m.initial_state)
+    m.state.restore(m.initial_state)
+    g = torch.Generator(device="cuda:0").manual_seed(4)
+    x0 = torch.randn(8, m.cfg.hidden, device="cuda:0", generator=g).to(torch.bfloat16)
+    assert torch.equal(m.body(x0), m2.body(x0))

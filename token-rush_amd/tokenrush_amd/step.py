@@ -67,8 +67,11 @@ class StepConfig:
     rope_theta: float = 1e7
     live: int = 8192           # tokens already in the KV cache when the step runs
     headroom: int = 1024       # cache rows past `live` for the steps that follow
+    layer_types: tuple = None  # a checkpoint's 'linear_attention' / 'full_attention' per layer
 
     def is_attention(self, li: int) -> bool:
+        if self.layer_types is not None:
+            return self.layer_types[li] == "full_attention"
         return li % self.attn_every == self.attn_every - 1
 
     @property
@@ -119,9 +122,15 @@ def _bf16(shape, std, gen, device, mean=0.0):
 
 
 class Layer:
+    """One layer's weights: proj (in_qkvz or qkv), out (out_proj / o_proj), the mixer's small
+    tensors, gate_up (pair layout, silu fused), down, ln1 / ln2. `split` holds the output sizes of
+    the matrices joined in proj (conv channels | z, or q | k | v)."""
+
     def __init__(self, cfg: StepConfig, li: int, gen, device):
         H = cfg.hidden
         self.attention = cfg.is_attention(li)
+        self.split = ((cfg.n_heads * 2 * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim) if self.attention
+                      else (cfg.gdn.conv_dim,))
         if self.attention:
             self.proj = _random_linear(cfg.attn_qkv, H, gen, device)
             self.out = _random_linear(H, cfg.attn_out, gen, device, split_k=4)       # weights.py:163-174
@@ -133,13 +142,44 @@ class Layer:
             self.out = _random_linear(H, cfg.gdn_out, gen, device, split_k=4)
             self.in_ba = _bf16((2 * g.gdn_v_heads, H), 0.02, gen, device)
             self.conv_w = _bf16((g.conv_dim, 4), 0.3, gen, device)
-            self.A = -torch.exp(torch.randn(g.gdn_v_heads, device=device, generator=gen))
+            self.A_log = torch.randn(g.gdn_v_heads, device=device, generator=gen)
+            self.A = -torch.exp(self.A_log)
             self.dt_bias = torch.randn(g.gdn_v_heads, device=device, generator=gen)
             self.norm_w = _bf16((g.gdn_v_dim,), 0.5, gen, device, mean=1.0)
         self.gate_up = _random_linear(2 * cfg.mlp, H, gen, device, layout="gate_up")   # silu fused in its epilogue
         self.down = _random_linear(H, cfg.mlp, gen, device, split_k=4)
         self.ln1 = _bf16((H,), 0.1, gen, device)
         self.ln2 = _bf16((H,), 0.1, gen, device)
+
+    @classmethod
+    def from_tensors(cls, cfg: StepConfig, li: int, tensors: dict, device):
+        """A layer from a packed checkpoint's tensors (weights.py:185-203)."""
+        from .checkpoint import SPLIT_K, linear
+        L = cls.__new__(cls)
+        dev = lambda n, dt=None: tensors[n].to(device=device, dtype=dt or tensors[n].dtype).contiguous()
+        p = f"layers.{li}."
+        L.attention = cfg.is_attention(li)
+        if L.attention:
+            m = p + "self_attn."
+            L.split = (cfg.n_heads * 2 * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim)
+            L.proj = linear(tensors, [m + "q_proj.weight", m + "k_proj.weight", m + "v_proj.weight"], device)
+            L.out = linear(tensors, m + "o_proj.weight", device, split_k=SPLIT_K)
+            L.q_norm_w, L.k_norm_w = dev(m + "q_norm.weight"), dev(m + "k_norm.weight")
+        else:
+            m = p + "linear_attn."
+            L.split = (cfg.gdn.conv_dim,)
+            L.proj = linear(tensors, [m + "in_proj_qkv.weight", m + "in_proj_z.weight"], device)
+            L.out = linear(tensors, m + "out_proj.weight", device, split_k=SPLIT_K)
+            L.in_ba = torch.cat([dev(m + "in_proj_b.weight"), dev(m + "in_proj_a.weight")])
+            L.conv_w = dev(m + "conv1d.weight").reshape(cfg.gdn.conv_dim, -1).contiguous()
+            L.A_log = dev(m + "A_log", torch.float32)
+            L.A = -torch.exp(L.A_log)
+            L.dt_bias = dev(m + "dt_bias", torch.float32)
+            L.norm_w = dev(m + "norm.weight")
+        L.gate_up = linear(tensors, [p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"], device, layout="gate_up")
+        L.down = linear(tensors, p + "mlp.down_proj.weight", device, split_k=SPLIT_K)
+        L.ln1, L.ln2 = dev(p + "input_layernorm.weight"), dev(p + "post_attention_layernorm.weight")
+        return L
 
     def weight_bytes(self) -> int:
         n = self.proj.nbytes + self.out.nbytes + self.gate_up.nbytes + self.down.nbytes
@@ -190,14 +230,20 @@ class VerifyModel:
     """Random-init weights and decode state of the config-5 hybrid (int4 g128 projections,
     bf16 scale/min) and the verify step. Weights are packed once at construction."""
 
-    def __init__(self, cfg: StepConfig = StepConfig(), device="cuda:0", seed: int = 0):
+    def __init__(self, cfg: StepConfig = StepConfig(), device="cuda:0", seed: int = 0, tensors: dict = None):
         self.cfg = cfg
         self.device = torch.device(device)
         gen = torch.Generator(device=self.device)
         gen.manual_seed(seed)
-        self.layers = [Layer(cfg, li, gen, self.device) for li in range(cfg.n_layers)]
-        self.final_norm = _bf16((cfg.hidden,), 0.1, gen, self.device)
-        self.lm_head = _random_linear(cfg.vocab, cfg.hidden, gen, self.device)
+        if tensors is None:
+            self.layers = [Layer(cfg, li, gen, self.device) for li in range(cfg.n_layers)]
+            self.final_norm = _bf16((cfg.hidden,), 0.1, gen, self.device)
+            self.lm_head = _random_linear(cfg.vocab, cfg.hidden, gen, self.device)
+        else:
+            from .checkpoint import linear
+            self.layers = [Layer.from_tensors(cfg, li, tensors, self.device) for li in range(cfg.n_layers)]
+            self.final_norm = tensors["norm.weight"].to(self.device)
+            self.lm_head = linear(tensors, "lm_head.weight", self.device)
         self.gdn_index, self.attn_index = {}, {}
         for li, L in enumerate(self.layers):
             d = self.attn_index if L.attention else self.gdn_index
@@ -233,6 +279,26 @@ class VerifyModel:
             h = L.down.partials(L.gate_up.silu_mul(n))
         _, n = add_rmsnorm(x, h, self.final_norm, cfg.eps)
         return n
+
+    @classmethod
+    def from_checkpoint(cls, path: str, device="cuda:0", seed: int = 0, **cfg_overrides):
+        """Weights from a packed checkpoint directory (weights.py:238-254 load_packed); the decode
+        state (rings, recurrent slots, KV cache) is random-initialised from `seed`."""
+        from .checkpoint import is_packed, read_config, read_tensors
+        if not is_packed(path):
+            raise RuntimeError(f"{path} is not a packed checkpoint (no tokenrush.json)")
+        return cls(read_config(path, **cfg_overrides), device=device, seed=seed, tensors=read_tensors(path))
+
+    def save_checkpoint(self, dst: str, meta: dict = None):
+        """Write the weights in the packed checkpoint format (weights.py:60-102)."""
+        from .checkpoint import layer_items, write_packed
+
+        def items():
+            for li, L in enumerate(self.layers):
+                yield from layer_items(L, li)
+            yield "norm.weight", self.final_norm
+            yield "lm_head.weight", self.lm_head.nibbles()
+        return write_packed(dst, items(), self.cfg, meta=meta)
 
     def body(self, x0: torch.Tensor) -> torch.Tensor:
         """x0 [M, hidden] bf16 -> logits [M, vocab] bf16, at the state's position and slot."""
