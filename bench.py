@@ -281,6 +281,10 @@ def main():
     tpath = os.path.join(ROOT, "profiles", "gate_up_m8_traffic.json")
     if os.path.exists(tpath):
         traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+    busy = {}
+    bpath = os.path.join(ROOT, "profiles", "gate_up_m8_mfma_valu.json")
+    if os.path.exists(bpath):   # rocprofv3 MfmaUtil / VALUBusy of the same kernel (a separate counter run)
+        busy = {k: v for k, v in json.load(open(bpath)).items() if k.endswith("_pct")}
     out = {
         "metric": "int4 verify GEMM HBM GB/s (% of peak) at M=1,8; verify+accept step latency us",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -301,7 +305,7 @@ def main():
         "config5_verify_step": c5,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "int4_gemm_kernel gate_up 34816x5120 M=8 (%.2f us)" % (k8["gate_up"] * 1e6)},
+                     "kernel": "int4_gemm_kernel gate_up 34816x5120 M=8 (%.2f us)" % (k8["gate_up"] * 1e6), **busy},
     }
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
