@@ -310,16 +310,20 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int r = rb + h;
+      f32x4 acc[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (active && r < r1) {
+#pragma unroll
+        for (int gw = 0; gw < GW; ++gw) tile_mac<MT, F16S>(buf[h].w[gw], buf[h].sm[gw], xa[gw], acc, kExp128);
+        min_fold<MT, GW, F16S>(buf[h].sm, Xa, slot16, acc);
+      }
+      // The refill is issued on every path (out-of-range offsets for inactive waves and past the
+      // range: zeros, no memory access), so every path has the same loads in flight and the
+      // compiler's wait before the next strip's compute covers that strip's loads only -- a
+      // refill under a branch made it wait for the other buffer's loads as well.
+      load_strip<GW>(buf[h], rsrc, active ? strip_off(r + 2) : oob, lane_off, sm_voff);
       if (r < r1) {
-        f32x4 acc[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (active) {
-#pragma unroll
-          for (int gw = 0; gw < GW; ++gw) tile_mac<MT, F16S>(buf[h].w[gw], buf[h].sm[gw], xa[gw], acc, kExp128);
-          min_fold<MT, GW, F16S>(buf[h].sm, Xa, slot16, acc);
-          load_strip<GW>(buf[h], rsrc, strip_off(r + 2), lane_off, sm_voff);
-        }
         float* ring = red + (size_t)half * RB * W * MT * 256;
         if (active) {
 #pragma unroll
