@@ -38,11 +38,84 @@ __device__ __forceinline__ void ws_gather(const T* src, int n, T* dst) {
   __syncthreads();
 }
 
-// Sequential fp32 sum of n LDS values (one thread; fixed left-to-right order).
-__device__ __forceinline__ float seq_sum(const float* v, int n) {
+// The same fixed left-to-right fp32 chains, run by a whole wave over values held in registers:
+// element j of the sequence is lane j % 64 of r[j / 64]. v_readlane brings each element to a
+// scalar register in index order, so every lane computes exactly the sequential result, without
+// a memory or LDS round trip per element (a lane-0 loop over LDS costs ~70 ns per element).
+// Callers pass zeros past the sequence's end: the chains are over non-negative values, to which
+// adding +0 changes nothing, so no per-element bound check (a divergent branch) is needed.
+__device__ __forceinline__ float lane_val(float v, int i) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+// The compiler would hoist every v_readlane of a chain ahead of its adds and run out of scalar
+// registers (spills); an empty asm that "writes" the value register every 16 elements keeps the
+// readlanes of one block after the previous block's adds.
+template <int R>
+__device__ __forceinline__ float wave_seq_sum(const float (&r)[R]) {
   float s = 0.f;
-  for (int i = 0; i < n; ++i) s = __fadd_rn(s, v[i]);
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    float x = r[k];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      if ((i & 15) == 0) asm volatile("" : "+v"(x), "+v"(s));
+      s = __fadd_rn(s, lane_val(x, i));
+    }
+  }
   return s;
+}
+// Running sums acc + x_0 + ... + x_j (left to right): lane i of pre[k] gets element 64 k + i's.
+// Every lane runs the same chain and stores each sum to the wave's LDS scratch (64 R floats; all
+// lanes write the same value to the same word), then reads back its own. The chain is not put
+// under a lane-0 branch: the compiler would sink the computation of the values that v_readlane
+// reads into that branch, leaving the other lanes' values uncomputed.
+template <int R>
+__device__ __forceinline__ void wave_seq_prefix(const float (&r)[R], float acc, float (&pre)[R], float* lds) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    float x = r[k];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      if ((i & 15) == 0) asm volatile("" : "+v"(x), "+v"(acc));
+      acc = __fadd_rn(acc, lane_val(x, i));
+      lds[64 * k + i] = acc;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int k = 0; k < R; ++k) pre[k] = lds[64 * k + lane];
+  __builtin_amdgcn_wave_barrier();
+}
+// The sequential inverse-CDF step: the first element whose running sum exceeds target, else the
+// last positive element (-1 if none); *base gets the running sum before it. Uniform result.
+// lds: 64 R floats of scratch.
+template <int R>
+__device__ __forceinline__ int wave_seq_search(const float (&r)[R], float acc, float target, float* base, float* lds) {
+  float pre[R];
+  wave_seq_prefix(r, acc, pre, lds);
+  int chosen = -1;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const unsigned long long m = __ballot(pre[k] > target);
+    if (chosen < 0 && m) chosen = 64 * k + __ffsll((long long)m) - 1;
+  }
+#pragma unroll
+  for (int k = R - 1; k >= 0; --k) {
+    const unsigned long long m = __ballot(r[k] > 0.f);
+    if (chosen < 0 && m) chosen = 64 * k + 63 - __clzll((long long)m);
+  }
+  chosen = __builtin_amdgcn_readfirstlane(chosen);
+  float b = acc;
+  const int pj = chosen - 1;
+  if (pj >= 0) {
+    float sel = pre[0];
+#pragma unroll
+    for (int k = 1; k < R; ++k) sel = (pj >> 6) == k ? pre[k] : sel;
+    b = lane_val(sel, pj & 63);
+  }
+  *base = b;
+  return chosen;
 }
 
 // Block-wide exclusive prefix sum of one int per thread (blockDim.x <= 1024), plus the total.
@@ -329,45 +402,28 @@ struct SampleArgs {
 };
 
 // One row's pick from its sorted top-64 (value desc, index asc), by wave 0: elementwise steps
-// on lane i = rank i, the three running sums sequentially on lane 0 (rank order), as the file
-// comment states. Returns the token in every lane of wave 0.
+// on lane i = rank i, the running sums in rank order by wave chains (the file comment's fixed
+// order). Returns the token in every lane of wave 0.
 __device__ int64_t sample_pick(const uint32_t* tk, const uint32_t* ti, float T, float top_p, int64_t top_k, float u) {
-  __shared__ float sv[kCand], sp[kCand], scum[kCand];
-  __shared__ float sZ, sTarget;
   const int i = threadIdx.x;  // 0..63
   if (!(T > 0.f)) return ti[0];
   const float temp = T > __uint_as_float(0x358637BDu) ? T : __uint_as_float(0x358637BDu);
-  sv[i] = __fdiv_rn(bf16_bits_to_f32(unord16(tk[i])), temp);
-  __builtin_amdgcn_wave_barrier();
-  const float e = texp(__fsub_rn(sv[i], sv[0]));
-  sp[i] = e;
-  __builtin_amdgcn_wave_barrier();
-  if (i == 0) sZ = seq_sum(sp, kCand);
-  __builtin_amdgcn_wave_barrier();
-  const float p = __fdiv_rn(e, sZ);
-  sp[i] = p;
-  __builtin_amdgcn_wave_barrier();
-  if (i == 0) {
-    float cum = 0.f;
-    for (int k = 0; k < kCand; ++k) {
-      cum = __fadd_rn(cum, sp[k]);
-      scum[k] = cum;
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  const bool keep = __fsub_rn(scum[i], p) < top_p && i < top_k;
-  sp[i] = keep ? p : 0.f;
-  __builtin_amdgcn_wave_barrier();
-  if (i == 0) {
-    float cum2 = 0.f;
-    for (int k = 0; k < kCand; ++k) {
-      cum2 = __fadd_rn(cum2, sp[k]);
-      scum[k] = cum2;
-    }
-    sTarget = __fmul_rn(u, cum2);
-  }
-  __builtin_amdgcn_wave_barrier();
-  const unsigned long long below = __ballot(scum[i] < sTarget);
+  const float sv = __fdiv_rn(bf16_bits_to_f32(unord16(tk[i])), temp);
+  const float e = texp(__fsub_rn(sv, lane_val(sv, 0)));
+  const float er[1] = {e};
+  const float p = __fdiv_rn(e, wave_seq_sum(er));
+  // cumulative sums in rank order; lane i keeps the sum through rank i
+  __shared__ float cum_s[kCand];
+  const float pr[1] = {p};
+  float cum[1];
+  wave_seq_prefix(pr, 0.f, cum, cum_s);
+  const bool keep = __fsub_rn(cum[0], p) < top_p && i < top_k;
+  const float pk[1] = {keep ? p : 0.f};
+  float cum2[1];
+  wave_seq_prefix(pk, 0.f, cum2, cum_s);
+  const float target = __fmul_rn(u, lane_val(cum2[0], kCand - 1));
+  const float mycum2 = cum2[0];
+  const unsigned long long below = __ballot(mycum2 < target);
   int pick = __popcll(below);
   if (pick > kCand - 1) pick = kCand - 1;
   return ti[pick];
@@ -496,25 +552,27 @@ __device__ float run_values(const ResidualArgs& a, int row, int ch, int lane, fl
   return s;
 }
 
-__device__ float chunk_total(float run_sum, float* lds64) {
+// Sum of the 64 lanes' run sums in lane order (every lane gets it).
+__device__ __forceinline__ float chunk_total(float run_sum) {
+  const float r[1] = {run_sum};
+  return wave_seq_sum(r);
+}
+
+// The row's chunk sums (n <= kMaxChunks) into registers of the wave: lane l gets chunks l,
+// l + 64, ..., zeros past n (agent-scope loads: other workgroups wrote them).
+__device__ __forceinline__ void gather_chunks(const float* src, int n, float (&r)[kMaxChunks / 64]) {
   const int lane = threadIdx.x & 63;
-  lds64[lane] = run_sum;
-  __syncthreads();
-  float t = 0.f;
-  if (lane == 0)
-    for (int i = 0; i < 64; ++i) t = __fadd_rn(t, lds64[i]);
-  __syncthreads();
-  return t;
+#pragma unroll
+  for (int k = 0; k < kMaxChunks / 64; ++k) r[k] = 64 * k + lane < n ? ws_ld(src + 64 * k + lane) : 0.f;
 }
 
 __global__ __launch_bounds__(64) void residual_phase2_kernel(ResidualArgs a) {
-  __shared__ float lds64[64];
   const int row = blockIdx.x / a.nch, ch = blockIdx.x % a.nch;
   const int lane = threadIdx.x;
   const float mx = ws_ld(a.rowmax + row);
   float vals[kRun];
   const float rs = run_values<0>(a, row, ch, lane, mx, 1.f, vals);
-  const float ct = chunk_total(rs, lds64);
+  const float ct = chunk_total(rs);
   const int K = a.M - 1;
   if (row < K) {
     const int64_t d = a.spec[row + 1];
@@ -523,9 +581,10 @@ __global__ __launch_bounds__(64) void residual_phase2_kernel(ResidualArgs a) {
   }
   if (lane == 0) ws_st(a.chunk_sum + blockIdx.x, ct);
   if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
-  __shared__ float cs[kMaxChunks];
-  ws_gather(a.chunk_sum + (size_t)row * a.nch, a.nch, cs);
-  if (lane == 0) ws_st(a.Z + row, seq_sum(cs, a.nch));
+  float cs[kMaxChunks / 64];
+  gather_chunks(a.chunk_sum + (size_t)row * a.nch, a.nch, cs);
+  const float Zrow = wave_seq_sum(cs);
+  if (lane == 0) ws_st(a.Z + row, Zrow);
   if (!arrive_last(a.cnt_all, a.M)) return;
   __shared__ float ed[32], zz[32], qd[32];
   __shared__ int dvalid[32];
@@ -547,105 +606,59 @@ __global__ __launch_bounds__(64) void residual_phase2_kernel(ResidualArgs a) {
 // Phase 3: one row j = n (the first rejected draft's row, or the bonus row K): chunk sums of
 // r, then the last workgroup draws the token with u[K] by a blocked inverse-CDF search.
 __global__ __launch_bounds__(64) void residual_phase3_kernel(ResidualArgs a) {
-  __shared__ float lds64[64];
-  __shared__ float runs[64];
+  __shared__ float pick_s;
+  __shared__ float scratch[kMaxChunks];
   const int ch = blockIdx.x, lane = threadIdx.x;
   const int K = a.M - 1;
   const int j = ws_ld(a.n_ws);
   const float mx = ws_ld(a.rowmax + j), Zj = ws_ld(a.Z + j);
   float vals[kRun];
   const float rs = j < K ? run_values<1>(a, j, ch, lane, mx, Zj, vals) : run_values<2>(a, j, ch, lane, mx, Zj, vals);
-  const float ct = chunk_total(rs, lds64);
+  const float ct = chunk_total(rs);
   if (lane == 0) ws_st(a.chunk_sum + ch, ct);
   if (!arrive_last(a.cnt_all, a.nch)) return;
-  __shared__ int s_pick_chunk;
-  __shared__ float s_acc;
-  __shared__ float s_target;
-  __shared__ int s_degenerate;
-  __shared__ float cs[kMaxChunks];
-  ws_gather(a.chunk_sum, a.nch, cs);
-  if (lane == 0) {
-    const float R = seq_sum(cs, a.nch);
-    s_degenerate = !(R > 0.f);
-    const float target = __fmul_rn(a.u[K], R);
-    // first chunk whose running total exceeds the target; else the last nonzero chunk
-    float cp = 0.f, cp_last = 0.f;
-    int c_found = -1, c_last = -1;
-    for (int c = 0; c < a.nch; ++c) {
-      const float t = cs[c];
-      if (t > 0.f) {
-        c_last = c;
-        cp_last = cp;
-      }
-      if (__fadd_rn(cp, t) > target) {
-        c_found = c;
-        break;
-      }
-      cp = __fadd_rn(cp, t);
-    }
-    s_pick_chunk = c_found >= 0 ? c_found : c_last;
-    s_acc = c_found >= 0 ? cp : cp_last;
-    s_target = target;
-  }
-  __syncthreads();
+  // blocked inverse-CDF search with u[K]: the chunk (first whose running total exceeds the
+  // target, else the last nonzero one), then its run, then the element; every sum sequential
+  float cs[kMaxChunks / 64];
+  gather_chunks(a.chunk_sum, a.nch, cs);
+  const float R = wave_seq_sum(cs);
+  const bool degenerate = !(R > 0.f);
+  const float target = __fmul_rn(a.u[K], R);
   int pick = -1;
-  if (!s_degenerate) {
-    const int c = s_pick_chunk;
+  if (!degenerate) {
+    float acc;
+    const int c = wave_seq_search(cs, 0.f, target, &acc, scratch);
     const float rsum = j < K ? run_values<1>(a, j, c, lane, mx, Zj, vals) : run_values<2>(a, j, c, lane, mx, Zj, vals);
-    runs[lane] = rsum;
-    lds64[lane] = 0.f;
-    __syncthreads();
-    // lane 0 finds the run, then the element, sequentially
-    __shared__ int s_run;
-    __shared__ float s_run_acc;
-    if (lane == 0) {
-      float acc = s_acc, acc_last = s_acc;
-      int t_found = -1, t_last = -1;
-      for (int t = 0; t < 64; ++t) {
-        if (runs[t] > 0.f) {
-          t_last = t;
-          acc_last = acc;
-        }
-        if (__fadd_rn(acc, runs[t]) > s_target) {
-          t_found = t;
-          break;
-        }
-        acc = __fadd_rn(acc, runs[t]);
-      }
-      s_run = t_found >= 0 ? t_found : t_last;
-      s_run_acc = t_found >= 0 ? acc : acc_last;
-    }
-    __syncthreads();
-    if (lane == s_run) {
-      float acc = s_run_acc;
+    const float rr[1] = {rsum};
+    float run_acc;
+    const int run = wave_seq_search(rr, acc, target, &run_acc, scratch);
+    if (lane == run) {
+      float x = run_acc;
       int last_nz = -1;
       for (int e = 0; e < kRun; ++e) {
         if (vals[e] > 0.f) last_nz = e;
-        acc = __fadd_rn(acc, vals[e]);
-        if (acc > s_target) {
+        x = __fadd_rn(x, vals[e]);
+        if (x > target) {
           pick = c * kChunk + lane * kRun + e;
           break;
         }
       }
       if (pick < 0) pick = c * kChunk + lane * kRun + last_nz;
-      lds64[0] = __int_as_float(pick);
+      pick_s = __int_as_float(pick);
     }
     __syncthreads();
-    pick = __float_as_int(lds64[0]);
+    pick = __float_as_int(pick_s);
   } else {
-    // degenerate residual (all zero): fall back to the row's argmax
-    pick = -2;
+    // degenerate residual (all zero): the row's argmax, first index on ties (keys are unique)
+    const uint16_t* lg = a.logits + (size_t)j * a.V;
+    uint64_t b = 0;
+    for (int i = lane; i < a.V; i += 64) {
+      const uint64_t k = vkey(ord16(lg[i]), i);
+      b = k > b ? k : b;
+    }
+    pick = (int)vkey_idx(wave_max_u64(b));
   }
   if (lane == 0) {
-    if (pick == -2) {
-      const uint16_t* lg = a.logits + (size_t)j * a.V;
-      uint64_t b = 0;
-      for (int i = 0; i < a.V; ++i) {
-        const uint64_t k = vkey(ord16(lg[i]), i);
-        b = k > b ? k : b;
-      }
-      pick = (int)vkey_idx(b);
-    }
     const int n = j;  // drafts a.spec[1..n] were accepted
     const int64_t base = *a.o.pos;
     *a.o.n_accepted = n;
