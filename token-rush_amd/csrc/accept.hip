@@ -160,6 +160,17 @@ __device__ float texp(float x) {
   return __fmul_rn(p, __int_as_float((ni + 127) << 23));
 }
 
+// One compare-exchange stage of a 64-lane bitonic sort (final order descending): partner lane
+// tid ^ STRIDE, direction from the SIZE-block (cross-lane moves on the VALU, xor_lane64).
+template <int SIZE, int STRIDE>
+__device__ __forceinline__ uint64_t sort_step(uint64_t key, int tid) {
+  const uint64_t other = xor_lane64<STRIDE>(key);
+  const bool desc = (tid & SIZE) == 0;
+  const bool lower = (tid & STRIDE) == 0;
+  const bool keep_max = desc == lower;
+  return keep_max ? (other > key ? other : key) : (other < key ? other : key);
+}
+
 // Top-64 of up to 256 * E items held E per thread, items of thread t preceding those of
 // thread t+1 in index order. Keys are ord16 values (0 = padding). Result in LDS out_k/out_i
 // (64 entries, value descending then index ascending); needs blockDim.x == 256.
@@ -239,14 +250,27 @@ __device__ void select_top64(const uint32_t (&k16)[E], const uint32_t (&idx)[E],
   if (tid < 64) {
     // bitonic sort of 64 (value desc, index asc) keys across the lanes of wave 0
     uint64_t key = vkey(sel_k[tid], sel_i[tid]);
-    for (int size = 2; size <= 64; size <<= 1)
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        const uint64_t other = __shfl_xor(key, stride);
-        const bool desc = (tid & size) == 0;  // final order: descending
-        const bool lower = (tid & stride) == 0;
-        const bool keep_max = desc == lower;
-        key = keep_max ? (other > key ? other : key) : (other < key ? other : key);
-      }
+    key = sort_step<2, 1>(key, tid);
+    key = sort_step<4, 2>(key, tid);
+    key = sort_step<4, 1>(key, tid);
+    key = sort_step<8, 4>(key, tid);
+    key = sort_step<8, 2>(key, tid);
+    key = sort_step<8, 1>(key, tid);
+    key = sort_step<16, 8>(key, tid);
+    key = sort_step<16, 4>(key, tid);
+    key = sort_step<16, 2>(key, tid);
+    key = sort_step<16, 1>(key, tid);
+    key = sort_step<32, 16>(key, tid);
+    key = sort_step<32, 8>(key, tid);
+    key = sort_step<32, 4>(key, tid);
+    key = sort_step<32, 2>(key, tid);
+    key = sort_step<32, 1>(key, tid);
+    key = sort_step<64, 32>(key, tid);
+    key = sort_step<64, 16>(key, tid);
+    key = sort_step<64, 8>(key, tid);
+    key = sort_step<64, 4>(key, tid);
+    key = sort_step<64, 2>(key, tid);
+    key = sort_step<64, 1>(key, tid);
     out_k[tid] = (uint32_t)(key >> 32);
     out_i[tid] = vkey_idx(key);
   }
@@ -257,14 +281,19 @@ __device__ void select_top64(const uint32_t (&k16)[E], const uint32_t (&idx)[E],
 // Wave-wide merge of two descending 64-key lists, one key per lane: lane i keeps the larger of
 // a[i] and b[63 - i] (the top 64 of the union, as a bitonic sequence), then a bitonic merge
 // sorts it descending. Keys are vkey()s: value descending, index ascending.
+template <int S>
+__device__ __forceinline__ uint64_t bitonic_step(uint64_t key, int lane) {
+  const uint64_t other = xor_lane64<S>(key);
+  const bool lower = (lane & S) == 0;
+  return lower ? (other > key ? other : key) : (other < key ? other : key);
+}
 __device__ __forceinline__ uint64_t bitonic_sort_desc(uint64_t key, int lane) {
-#pragma unroll
-  for (int stride = 32; stride > 0; stride >>= 1) {
-    const uint64_t other = __shfl_xor(key, stride);
-    const bool lower = (lane & stride) == 0;
-    key = lower ? (other > key ? other : key) : (other < key ? other : key);
-  }
-  return key;
+  key = bitonic_step<32>(key, lane);
+  key = bitonic_step<16>(key, lane);
+  key = bitonic_step<8>(key, lane);
+  key = bitonic_step<4>(key, lane);
+  key = bitonic_step<2>(key, lane);
+  return bitonic_step<1>(key, lane);
 }
 __device__ __forceinline__ uint64_t merge_top64(uint64_t a, uint64_t b_rev, int lane) {
   return bitonic_sort_desc(a > b_rev ? a : b_rev, lane);
@@ -277,19 +306,25 @@ __device__ void merge_lists_top64(const uint32_t* src, int n, uint32_t* out_k, u
   constexpr int kPerWave = 16;  // lists per wave: n <= 64 with 4 waves
   __shared__ uint64_t wres[16][kCand];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  // every list of this wave is loaded before any merge: independent loads, one round trip
+  // every list of this wave is loaded before any merge: independent loads, one round trip. The
+  // loads are unconditional (lists past n re-read list n - 1 and are dropped afterwards): an
+  // agent-scope load under a condition cannot be speculated, and the branch around each one
+  // made the compiler wait for it before the next.
   uint32_t kv[kPerWave], iv[kPerWave];
 #pragma unroll
   for (int j = 0; j < kPerWave; ++j) {
     const int c = wid + j * nw;
-    const uint32_t* l = src + (size_t)c * kCand * 2 + 2 * (kCand - 1 - lane);  // reversed: ascending
-    kv[j] = c < n ? ws_ld(l) : 0u;
-    iv[j] = c < n ? ws_ld(l + 1) : 0xFFFFFFFFu;
+    const int cc = c < n ? c : n - 1;
+    const uint64_t* l = (const uint64_t*)(src + (size_t)cc * kCand * 2 + 2 * (kCand - 1 - lane));  // reversed: ascending
+    const uint64_t v = ws_ld(l);  // (key16, index) pair
+    kv[j] = c < n ? (uint32_t)v : 0u;
+    iv[j] = c < n ? (uint32_t)(v >> 32) : 0xFFFFFFFFu;
   }
+  // merging a padding list (all keys minimal) leaves acc unchanged, so every merge runs: no
+  // branch, no wait for the loads of lists that are not merged yet
   uint64_t acc = bitonic_sort_desc(vkey(kv[0], iv[0]), lane);
 #pragma unroll
-  for (int j = 1; j < kPerWave; ++j)
-    if (wid + j * nw < n) acc = merge_top64(acc, vkey(kv[j], iv[j]), lane);
+  for (int j = 1; j < kPerWave; ++j) acc = merge_top64(acc, vkey(kv[j], iv[j]), lane);
   wres[wid][lane] = acc;
   __syncthreads();
   if (wid == 0) {
@@ -563,7 +598,11 @@ __device__ __forceinline__ float chunk_total(float run_sum) {
 __device__ __forceinline__ void gather_chunks(const float* src, int n, float (&r)[kMaxChunks / 64]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int k = 0; k < kMaxChunks / 64; ++k) r[k] = 64 * k + lane < n ? ws_ld(src + 64 * k + lane) : 0.f;
+  for (int k = 0; k < kMaxChunks / 64; ++k) {
+    const int c = 64 * k + lane;
+    const float v = ws_ld(src + (c < n ? c : n - 1));  // unconditional (see merge_lists_top64)
+    r[k] = c < n ? v : 0.f;
+  }
 }
 
 __global__ __launch_bounds__(64) void residual_phase2_kernel(ResidualArgs a) {

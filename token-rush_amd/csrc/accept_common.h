@@ -40,12 +40,42 @@ __device__ __forceinline__ uint64_t vkey(uint32_t k16, uint32_t idx) {
 }
 __device__ __forceinline__ uint32_t vkey_idx(uint64_t k) { return 0xFFFFFFFFu - (uint32_t)k; }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t w = __shfl_xor(v, o);
-    v = w > v ? w : v;
+// v of lane l ^ S (S = 1, 2, ..., 32) on the VALU, without the LDS crossbar of __shfl_xor:
+// quad_perm for 1 and 2, quad_perm [3,2,1,0] then row_half_mirror for 4 (l -> (l ^ 3) ^ 7),
+// row_ror:8 for 8, the permlane swaps for 16 and 32. A swap returns the lane's own value in one
+// result and its partner's in the other; taking the one that differs from the own value (or
+// either, when they are equal) gives the partner's value. All lanes of the wave must execute it.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int S>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  if constexpr (S == 1) return dpp_u32<0xB1>(v);
+  else if constexpr (S == 2) return dpp_u32<0x4E>(v);
+  else if constexpr (S == 4) return dpp_u32<0x141>(dpp_u32<0x1B>(v));
+  else if constexpr (S == 8) return dpp_u32<0x128>(v);
+  else if constexpr (S == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return r[0] != v ? r[0] : r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return r[0] != v ? r[0] : r[1];
   }
+}
+template <int S>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+  return ((uint64_t)xor_lane<S>((uint32_t)(v >> 32)) << 32) | xor_lane<S>((uint32_t)v);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  uint64_t w;
+  w = xor_lane64<32>(v); v = w > v ? w : v;
+  w = xor_lane64<16>(v); v = w > v ? w : v;
+  w = xor_lane64<8>(v); v = w > v ? w : v;
+  w = xor_lane64<4>(v); v = w > v ? w : v;
+  w = xor_lane64<2>(v); v = w > v ? w : v;
+  w = xor_lane64<1>(v); v = w > v ? w : v;
   return v;
 }
 

@@ -393,10 +393,19 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     __shared__ int64_t pred[32], spec[32];
     const int nwv = blockDim.x >> 6;
     for (int m = threadIdx.x >> 6; m < a.M; m += nwv) {
+      // up to 8 keys per lane loaded unconditionally (clamped index), so all are in flight at
+      // once; a loop of loads under its bound check waited for each in turn
       uint64_t best = 0;
-      for (int g = lane; g < (int)gridDim.x; g += 64) {
-        const uint64_t k = ws_ld(a.am_keys + (size_t)g * a.M + m);
-        best = k > best ? k : best;
+      const int grid = (int)gridDim.x;
+      for (int g0 = 0; g0 < grid; g0 += 512) {
+        uint64_t k[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int g = g0 + lane + 64 * q;
+          k[q] = ws_ld(a.am_keys + (size_t)(g < grid ? g : grid - 1) * a.M + m);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) best = (g0 + lane + 64 * q < grid && k[q] > best) ? k[q] : best;
       }
       best = wave_max_u64(best);
       if (lane == 0) {
