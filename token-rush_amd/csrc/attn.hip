@@ -33,6 +33,7 @@ constexpr int kKPitch = kAttnD + 8;     // bf16 elements per K row in LDS
 constexpr int kVPitch = kAttnBlk + 4;   // bf16 elements per V^T row (one d) in LDS
 constexpr float kFp8Max = 448.f;
 constexpr int kMaxSplit = 256;  // key-range splits of one flash-decoding call
+static_assert(kMaxSplit <= kAttnD, "the combine kernel gives each split one thread");
 
 // ------------------------------------------------------------------ fp8 e4m3fn (OCP) helpers
 
@@ -110,6 +111,13 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
   const uint16_t* src = isq ? row + (size_t)head * 2 * kAttnD : row + (size_t)a.HQ * 2 * kAttnD + (size_t)j * kAttnD;
   const uint16_t* w = isq ? a.qn_w : a.kn_w;
   const int d0 = 4 * lane;
+  uint16_t cs_raw[4], sn_raw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (d0 + i) % (a.RD / 2);
+    cs_raw[i] = a.cos[(size_t)p * a.RD + r];
+    sn_raw[i] = a.sin[(size_t)p * a.RD + r];
+  }
   float x[4], wv[4];
   {
     const uint2 xu = *(const uint2*)(src + d0), wu = *(const uint2*)(w + d0);
@@ -129,7 +137,8 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
   float xn[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xn[i] = bf16r_a(x[i] * inv * (1.f + wv[i]));
-  // partial rope on dims < RD: dim r pairs with r + RD / 2 (a lane RD / 8 lanes away)
+  // partial rope on dims < RD: dim r pairs with r + RD / 2 (a lane RD / 8 lanes away). The
+  // table entries were loaded with x (in-range indices for every dim, used where d < RD).
   const int half = a.RD / 2;
   float out[4];
 #pragma unroll
@@ -138,9 +147,7 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
     const int d = d0 + i;
     out[i] = xn[i];
     if (d < a.RD) {
-      const int r = d < half ? d : d - half;
-      const float c = bf16_bits_to_f32(a.cos[(size_t)p * a.RD + r]);
-      const float s = bf16_bits_to_f32(a.sin[(size_t)p * a.RD + r]);
+      const float c = bf16_bits_to_f32(cs_raw[i]), s = bf16_bits_to_f32(sn_raw[i]);
       out[i] = d < half ? bf16r_a(bf16r_a(xn[i] * c) + bf16r_a(-other * s))
                         : bf16r_a(bf16r_a(xn[i] * c) + bf16r_a(other * s));
     }
@@ -377,44 +384,53 @@ struct AttnReduceArgs {
   int HQ, nsplit, ld;
 };
 
-// One workgroup of D threads per (token, query head).
+// One workgroup of D threads per (token, query head). Every load is issued up front: the split
+// accumulators of this thread's dimension in batches of 64 (clamped indices past nsplit, weight
+// 0), one split's (m, l) per thread, and the gate; the split maximum and the weighted total are
+// block reductions.
 __global__ __launch_bounds__(kAttnD) void attn_reduce_kernel(AttnReduceArgs a) {
-  __shared__ float wsh[kMaxSplit], lsh;
-  const int h = blockIdx.x, d = threadIdx.x;
-  // split weights exp(m_s - max) once per workgroup (fixed order), then each thread sums its
-  // dimension over the splits with all loads issued ahead
-  if (d < 64) {
-    float mm = -INFINITY;
-    for (int s = d; s < a.nsplit; s += 64) mm = fmaxf(mm, a.m_part[(size_t)h * a.nsplit + s]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
-    for (int s = d; s < a.nsplit; s += 64) {
-      const float m = a.m_part[(size_t)h * a.nsplit + s];
-      wsh[s] = m == -INFINITY ? 0.f : expf(m - mm);
-    }
-  }
-  __syncthreads();
-  if (d == 0) {
-    float lt = 0.f;
-    for (int s = 0; s < a.nsplit; ++s) lt += wsh[s] * a.l_part[(size_t)h * a.nsplit + s];
-    lsh = lt;
-  }
-  const float* ap = a.acc_part + (size_t)h * a.nsplit * kAttnD + d;
-  float o = 0.f;
-  int s = 0;
-  for (; s + 8 <= a.nsplit; s += 8) {
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = ap[(size_t)(s + i) * kAttnD];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o += wsh[s + i] * v[i];
-  }
-  for (; s < a.nsplit; ++s) o += wsh[s] * ap[(size_t)s * kAttnD];
-  __syncthreads();
-  const float lt = lsh;
-  o = bf16r_a(o / lt);
+  constexpr int kB = 64;
+  __shared__ float wsh[kMaxSplit], red[kAttnD / 64];
+  const int h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
+  const int ns = a.nsplit;
   const int t = h / a.HQ, hh = h % a.HQ;
-  const float gate = bf16_bits_to_f32(a.qkv[(size_t)t * a.ld + (size_t)hh * 2 * kAttnD + kAttnD + d]);
+  const uint16_t graw = a.qkv[(size_t)t * a.ld + (size_t)hh * 2 * kAttnD + kAttnD + d];
+  const float* ap = a.acc_part + (size_t)h * ns * kAttnD + d;
+  float v[kB];
+#pragma unroll
+  for (int i = 0; i < kB; ++i) v[i] = ap[(size_t)min(i, ns - 1) * kAttnD];
+  const int sc = min(d, ns - 1);
+  const float m_s = a.m_part[(size_t)h * ns + sc], l_s = a.l_part[(size_t)h * ns + sc];
+  const bool mine = d < ns;  // ns <= kMaxSplit == kAttnD
+  // maximum over the splits
+  float mm = mine ? m_s : -INFINITY;
+  mm = fmaxf(mm, __shfl_xor(mm, 32));
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+  if (lane == 0) red[wave] = mm;
+  __syncthreads();
+  mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float w = mine && m_s != -INFINITY ? expf(m_s - mm) : 0.f;
+  if (mine) wsh[d] = w;
+  // total weight sum_s w_s l_s
+  float lt = sum_wave(w * l_s);
+  __syncthreads();  // red[] reads done, wsh[] written
+  if (lane == 0) red[wave] = lt;
+  __syncthreads();
+  lt = ((red[0] + red[1]) + red[2]) + red[3];
+  float o = 0.f;
+#pragma unroll
+  for (int i = 0; i < kB; ++i)
+    if (i < ns) o += wsh[i] * v[i];
+  for (int s0 = kB; s0 < ns; s0 += kB) {  // nsplit > 64: further batches
+#pragma unroll
+    for (int i = 0; i < kB; ++i) v[i] = ap[(size_t)min(s0 + i, ns - 1) * kAttnD];
+#pragma unroll
+    for (int i = 0; i < kB; ++i)
+      if (s0 + i < ns) o += wsh[s0 + i] * v[i];
+  }
+  o = bf16r_a(o / lt);
+  const float gate = bf16_bits_to_f32(graw);
   const float g = bf16r_a(1.f / (1.f + expf(-gate)));
   a.out[(size_t)h * kAttnD + d] = f32_to_bf16_bits(o * g);
 }

@@ -43,6 +43,7 @@ constexpr int kGdnBV = 32;   // value columns per step workgroup
 constexpr int kGdnNVB = kGdnV / kGdnBV;
 constexpr int kGdnMaxM = 8;  // tokens per step (the reference's MP, fused.py:150)
 constexpr int kGdnThreads = 256;
+static_assert(kGdnMaxM * kGdnBV == kGdnThreads, "one v element per thread in the step prologue");
 
 struct GdnArgs {
   const uint16_t* qkvz;    // [M, ld] bf16: q | k | v | z
@@ -205,20 +206,35 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) S[j] = *(const float4*)(src + (size_t)(k0 + j) * kGdnV);
   }
-  for (int e = tid; e < M * kGdnK; e += kGdnThreads) {
-    const int t = e / kGdnK, c = e % kGdnK;
-    cq[t][c] = a.qk[(size_t)t * 2 * QK + ih * kGdnK + c];
-    ck[t][c] = a.qk[(size_t)t * 2 * QK + QK + ih * kGdnK + c];
-  }
-  for (int e = tid; e < M * kGdnBV; e += kGdnThreads) {
-    const int t = e / kGdnBV, c = e % kGdnBV;
-    cv[t][c] = bf16_bits_to_f32(a.vconv[(size_t)t * VAL + hv * kGdnV + vb * kGdnBV + c]);
-  }
-  if (tid < M) {
-    const float b = a.gates[(size_t)tid * 2 * a.HV + hv];
-    const float av = a.gates[(size_t)tid * 2 * a.HV + a.HV + hv];
-    beta_s[tid] = bf16r(1.f / (1.f + expf(-b)));
-    decay_s[tid] = expf(a.A[hv] * softplus_f(av + a.dt_bias[hv]));
+  // q / k, v and the gates: every load issued at once (a loop with a runtime bound waited for
+  // each iteration's loads); indices past M are clamped to token M - 1 and not stored
+  {
+    constexpr int kQK = kGdnMaxM * kGdnK / kGdnThreads;  // 4
+    float qv[kQK], kv2[kQK];
+#pragma unroll
+    for (int q = 0; q < kQK; ++q) {
+      const int e = tid + kGdnThreads * q, t = min(e / kGdnK, M - 1), c = e % kGdnK;
+      qv[q] = a.qk[(size_t)t * 2 * QK + ih * kGdnK + c];
+      kv2[q] = a.qk[(size_t)t * 2 * QK + QK + ih * kGdnK + c];
+    }
+    const int ev = tid, tv = min(ev / kGdnBV, M - 1), cvi = ev % kGdnBV;  // kGdnMaxM * kGdnBV == kGdnThreads
+    const uint16_t vraw = a.vconv[(size_t)tv * VAL + hv * kGdnV + vb * kGdnBV + cvi];
+    const int tg = min(tid, M - 1);
+    const float b = a.gates[(size_t)tg * 2 * a.HV + hv];
+    const float av = a.gates[(size_t)tg * 2 * a.HV + a.HV + hv];
+#pragma unroll
+    for (int q = 0; q < kQK; ++q) {
+      const int e = tid + kGdnThreads * q, t = e / kGdnK, c = e % kGdnK;
+      if (t < M) {
+        cq[t][c] = qv[q];
+        ck[t][c] = kv2[q];
+      }
+    }
+    if (ev / kGdnBV < M) cv[ev / kGdnBV][cvi] = bf16_bits_to_f32(vraw);
+    if (tid < M) {
+      beta_s[tid] = bf16r(1.f / (1.f + expf(-b)));
+      decay_s[tid] = expf(a.A[hv] * softplus_f(av + a.dt_bias[hv]));
+    }
   }
   __syncthreads();
 
