@@ -302,6 +302,12 @@ def main():
         "layer_set_us_by_M": {1: round(sum(k1.values()) * 1e6, 2), 8: round(sum(k8.values()) * 1e6, 2), **sweep},
         "accept_us": acc,
         "verify_accept_us_m8": round(sum(k8.values()) * 1e6 + acc["greedy_m8"], 2),
+        # one layer set's GEMMs at the config's M plus its accept: configs 3 (M = 8, greedy /
+        # sampled / residual) and 4 (M = 32 tree)
+        "verify_accept_us": {"greedy_m8": round(sum(k8.values()) * 1e6 + acc["greedy_m8"], 2),
+                             "sampled_m8": round(sum(k8.values()) * 1e6 + acc["sampled_m8"], 2),
+                             "residual_m8": round(sum(k8.values()) * 1e6 + acc["residual_m8"], 2),
+                             "tree_m32": round(sweep.get(32, float("nan")) + acc["tree_m32"], 2)},
         "config5_verify_step": c5,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
