@@ -149,27 +149,33 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
   float acc[kGdnMaxM];
 #pragma unroll
   for (int t = 0; t < kGdnMaxM; ++t) acc[t] = 0.f;
+  // three 512-element chunks per pass (a quarter of hidden 5120 is 2.5), every load of a pass
+  // issued first; chunks past the quarter load zeros (offsets beyond the buffer resources)
   typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-  for (int e = q0 + 8 * lane; e < q1; e += 8 * 64 * 2) {
-    // two chunks per iteration, every load issued before the arithmetic
-    const int e1 = e + 8 * 64;
-    const bool in1 = e1 < q1;
-    const uint4 w0v = *(const uint4*)(wrow + e);
-    const uint4 w1v = in1 ? *(const uint4*)(wrow + e1) : make_uint4(0, 0, 0, 0);
-    u4 x0[kGdnMaxM], x1[kGdnMaxM];
+  constexpr int kCh = 3;
+  const auto wr = gdn_rsrc(wrow, (size_t)a.hidden * 2);
+  for (int e = q0 + 8 * lane; e < q1; e += kCh * 8 * 64) {
+    u4 wv[kCh], xv[kCh][kGdnMaxM];
 #pragma unroll
-    for (int t = 0; t < kGdnMaxM; ++t) {
-      x0[t] = __builtin_amdgcn_raw_buffer_load_b128(xr, t < M ? (t * a.hidden + e) * 2 : 0x7FFFFFF0, 0, 0);
-      x1[t] = __builtin_amdgcn_raw_buffer_load_b128(xr, (t < M && in1) ? (t * a.hidden + e1) * 2 : 0x7FFFFFF0, 0, 0);
+    for (int c = 0; c < kCh; ++c) {
+      const int ec = e + c * 8 * 64;
+      const bool in = ec < q1;
+      wv[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, in ? ec * 2 : 0x7FFFFFF0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < kGdnMaxM; ++t)
+        xv[c][t] = __builtin_amdgcn_raw_buffer_load_b128(xr, (in && t < M) ? (t * a.hidden + ec) * 2 : 0x7FFFFFF0, 0, 0);
     }
-    const uint32_t wa[8] = {w0v.x, w0v.y, w0v.z, w0v.w, w1v.x, w1v.y, w1v.z, w1v.w};
 #pragma unroll
-    for (int t = 0; t < kGdnMaxM; ++t) {
-      const uint32_t xw[8] = {x0[t].x, x0[t].y, x0[t].z, x0[t].w, x1[t].x, x1[t].y, x1[t].z, x1[t].w};
+    for (int c = 0; c < kCh; ++c) {
+      const uint32_t wa[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
 #pragma unroll
-      for (int c = 0; c < 8; ++c)
-        acc[t] += bf16_bits_to_f32(xw[c] & 0xFFFFu) * bf16_bits_to_f32(wa[c] & 0xFFFFu) +
-                  bf16_bits_to_f32(xw[c] >> 16) * bf16_bits_to_f32(wa[c] >> 16);
+      for (int t = 0; t < kGdnMaxM; ++t) {
+        const uint32_t xw[4] = {xv[c][t].x, xv[c][t].y, xv[c][t].z, xv[c][t].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc[t] += bf16_bits_to_f32(xw[q] & 0xFFFFu) * bf16_bits_to_f32(wa[q] & 0xFFFFu) +
+                    bf16_bits_to_f32(xw[q] >> 16) * bf16_bits_to_f32(wa[q] >> 16);
+      }
     }
   }
 #pragma unroll
