@@ -264,7 +264,7 @@ def tree_accept(pred: np.ndarray, tokens: np.ndarray, parent: np.ndarray, pos: i
             "tokens": [int(tokens[k]) for k in path[1:]] + [tok], "commit": path}
 
 
-# ------------------------------------------------------------------ synthetic inputs
+# ------------------------------------------------------------------ synthetic inputs (benchmark configs 3-4)
 
 def planted_logits(M: int, V: int, seed: int, drafts_from: np.ndarray = None, prefix: int = 0, sigma: float = 2.0):
     """bf16-valued logits [M, V] ~ N(0, sigma^2); when drafts_from (int64 [M]) is given, the

@@ -193,11 +193,11 @@ def gemm_fold(x, packed, scale, mn) -> np.ndarray:
     return acc
 
 
-# ------------------------------------------------------------------ synthetic inputs
+# ------------------------------------------------------------------ synthetic inputs (benchmark configs)
 
 def make_weights(N: int, K: int, seed: int, dtype: str = "fp16"):
     """Codes uniform in 0..15 (engine packing), scale ~U(0.002, 0.02), min ~U(-0.15, -0.01),
-    rounded to `dtype`."""
+    rounded to `dtype` (benchmark configs 1-2)."""
     rng = np.random.default_rng(seed)
     codes = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
     scale = round_to(rng.uniform(0.002, 0.02, size=(N, K // GROUP)).astype(np.float32), dtype)

@@ -1,6 +1,6 @@
 """Parity of the on-device accept/commit kernels with the CPU oracle (oracle/accept.py), called
 through the C-ABI (tokenrush_amd.sample / tokenrush_amd.accept -> libtrhip.so). Token ids,
-accepted lengths, positions and commit indices must be bit-exact. Covers BASELINE configs 3-4
+accepted lengths, positions and commit indices must be bit-exact. Covers benchmark configs 3-4
 at full size (V = 248320), ragged and tiny vocabularies, ties, every draft prefix length,
 graph replay and repeated calls (the workspace counters reset themselves)."""
 import numpy as np
@@ -60,7 +60,7 @@ def test_argmax_rows(dev, M, V):
 
 @pytest.mark.parametrize("prefix", range(8))
 def test_accept_greedy_config3(dev, prefix):
-    """BASELINE config 3 greedy: 7 drafts, argmax planted on a prefix of length 0..7."""
+    """benchmark config 3 greedy: 7 drafts, argmax planted on a prefix of length 0..7."""
     from tokenrush_amd.accept import accept_greedy
     say(f"greedy prefix={prefix}")
     rng = np.random.default_rng(prefix)
@@ -137,7 +137,7 @@ def _draft_probs(K, V, seed):
 
 @pytest.mark.parametrize("seed", range(6))
 def test_accept_residual_config3(dev, seed):
-    """BASELINE config 3 stochastic: 7 drafts, q = softmax of N(0, 4) logits, u [8] given."""
+    """benchmark config 3 stochastic: 7 drafts, q = softmax of N(0, 4) logits, u [8] given."""
     from tokenrush_amd.accept import accept_residual
     say(f"residual seed={seed}")
     rng = np.random.default_rng(300 + seed)
@@ -176,7 +176,7 @@ def test_accept_residual_small_vocab_many_draws(dev):
 
 @pytest.mark.parametrize("seed", range(5))
 def test_accept_tree_config4(dev, seed):
-    """32-node tree (branching <= 4, depth <= 7), logits [32, V]."""
+    """benchmark config 4: 32-node tree (branching <= 4, depth <= 7), logits [32, V]."""
     from tokenrush_amd.accept import accept_tree
     say(f"tree seed={seed}")
     parent = oa.random_tree(32, seed=seed)

@@ -180,7 +180,7 @@ def test_dequant_bit_exact(dev, dtype):
 
 
 def test_config1_full_size(dev):
-    """M=1, 5120 x 5120, fp16 scale/min."""
+    """benchmark config 1: M=1, 5120 x 5120, fp16 scale/min."""
     from tokenrush_amd import gfx950
     say("config1")
     p, s, m = o.make_weights(5120, 5120, seed=101, dtype="fp16")
@@ -191,7 +191,7 @@ def test_config1_full_size(dev):
 
 @pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
 def test_config2_layer_set_m8(dev, N, K):
-    """one layer's projection set at M=8, fp16 scale/min, full size."""
+    """benchmark config 2: one layer's projection set at M=8, fp16 scale/min, full size."""
     from tokenrush_amd import gfx950
     say(f"config2 N={N} K={K}")
     p, s, m = o.make_weights(N, K, seed=200 + N % 97, dtype="fp16")

@@ -1,4 +1,4 @@
-"""One speculative verify step of the 64-layer hybrid model, random-init,
+"""One speculative verify step of the 64-layer hybrid model (benchmark config 5), random-init,
 capturable as a single hipGraph.
 
 The layer body follows Engine._body (reference tokenrush/model.py:211-260) with the verify-path
@@ -108,7 +108,7 @@ SMALL = StepConfig(n_layers=4, hidden=512, mlp=1024, vocab=4096, gdn_k_heads=2, 
 
 
 def _random_linear(N, K, gen, device, split_k=1, scale_dtype=torch.bfloat16, layout="rows"):
-    """Codes uniform in 0..15, scale ~U(0.002, 0.02), min ~U(-0.15, -0.01)."""
+    """Codes uniform in 0..15, scale ~U(0.002, 0.02), min ~U(-0.15, -0.01) (benchmark configs)."""
     q = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=device, generator=gen)
     s = (torch.rand(N, K // 128, device=device, generator=gen) * 0.018 + 0.002).to(scale_dtype)
     m = (torch.rand(N, K // 128, device=device, generator=gen) * 0.14 - 0.15).to(scale_dtype)
