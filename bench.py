@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 verify path on one MI355X.
 
-Workload: one layer's int4 g128 projection set -- QKV-like 7168x5120,
+Workload (benchmark config 2): one layer's int4 g128 projection set -- QKV-like 7168x5120,
 O 5120x6144, fused gate/up 34816x5120, down 5120x17408, fp16 scale/min -- scored against
 M = 8 verify rows (1 committed + 7 drafts), bf16 x ~ N(0, 1), synthetic seeded data. As in the
 reference engine (weights.py:163-174, model.py:211-260), the hidden-sized outputs (O, down) are
@@ -15,7 +15,7 @@ value       whole-job algorithmic bytes / wall time of the timed steps (GB/s); b
 roofline    the dominant kernel (gate/up, 53% of the bytes): its algorithmic bytes / its mean
             duration, measured with HIP events around a graph of back-to-back launches of that
             kernel alone over all weight copies, on the launch stream; vs 8 TB/s.
-accept      on-device accept latency (BASELINE config 3 and 4): mean per launch over a graph of
+accept      on-device accept latency (benchmark config 3 and 4): mean per launch over a graph of
             back-to-back calls.
 config5     one verify step of the random-init 64-layer hybrid at M = 8 (257 int4 GEMMs, split-K
             partial consumers, 48 GDN steps, 16 FP8 attention layers over 8192 live tokens, lm_head,
@@ -113,7 +113,7 @@ def kernel_means(torch, gfx950, copies, xs, reps=4):
 
 
 def accept_latency(torch, dev):
-    """Mean microseconds per launch of the accept kernels at BASELINE configs 3 and 4."""
+    """Mean microseconds per launch of the accept kernels at benchmark configs 3 and 4."""
     from tokenrush_amd.accept import AcceptState, accept_greedy, accept_residual, accept_sampled, accept_tree
     from tokenrush_amd.sample import SamplingParams, workspace
     gen = torch.Generator(device=dev)
@@ -144,7 +144,7 @@ def accept_latency(torch, dev):
 
 
 def config5_step(torch, dev, M=M_VERIFY, reps=10):
-    """one verify step of the random-init 64-layer hybrid (48 GDN + 16 attention
+    """benchmark config 5: one verify step of the random-init 64-layer hybrid (48 GDN + 16 attention
     layers, int4 g128 weights, GDN steps and FP8 attention over 8192 live tokens) + lm_head + greedy
     accept/commit, captured as one hipGraph (tokenrush_amd.step). Returns the replay time and the weight-streaming rate."""
     from tokenrush_amd.accept import AcceptState
@@ -290,7 +290,7 @@ def main():
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(wall8 * 1e3 / a.steps, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int4 x bf16 -> fp32 acc (fp16 scale/min)", "data": "synthetic",
-        "config": {"workload": "BASELINE config 2: one layer set (qkv 7168x5120, o 5120x6144 partials, gate_up "
+        "config": {"workload": "benchmark config 2: one layer set (qkv 7168x5120, o 5120x6144 partials, gate_up "
                                "34816x5120, down 5120x17408 partials), M=8, weights cycled over %d copies (%.2f GB)"
                                % (n_copies, n_copies * copy_bytes / 1e9), "M": M_VERIFY, "parallelism": "none"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
