@@ -25,7 +25,10 @@ namespace tr {
 // ------------------------------------------------------------------ shared helpers
 
 constexpr int kCand = 64;          // sampling candidates (tokenrush/sample.py:12)
-constexpr int kTopChunk = 4096;    // elements per workgroup in the argmax / top-64 kernels
+constexpr int kTopChunk = 4096;    // elements per workgroup in the top-64 kernel
+// elements per workgroup in the argmax kernel: 4096 up to 8 rows, 16384 above (about 500
+// workgroups either way: enough to stream the logits, few per-row handshakes)
+constexpr int kArgChunkSmall = 4096, kArgChunkLarge = 16384;
 constexpr int kRun = 16, kChunk = 1024;
 constexpr int kMaxChunks = 256;    // 1024-element chunks per row: V <= 262144
 constexpr int kCntStride = 64;     // ints between workspace counters (one 256-byte line each)
@@ -352,28 +355,34 @@ struct ArgmaxArgs {
   AcceptOut o;
 };
 
+template <int kArgChunk>
 __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
   const int row = blockIdx.x / a.nch, ch = blockIdx.x % a.nch;
-  const int beg = ch * kTopChunk;
+  const int beg = ch * kArgChunk;
   const uint16_t* lg = a.logits + (size_t)row * a.V;
   uint64_t best = 0;
   if ((a.V & 7) == 0) {
-    // 16-byte loads: thread t reads elements beg + 8 t + 2048 h + (0..7), h = 0, 1
+    // 16-byte loads: thread t reads elements beg + 8 t + 2048 h + (0..7), h = 0..7, all issued at
+    // once (past the row end: the row's last 8 elements again, not counted)
+    constexpr int kH = kArgChunk / 2048;
+    uint4 v[kH];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i0 = beg + h * (kTopChunk / 2) + threadIdx.x * 8;
-      if (i0 < a.V) {
-        const uint4 v = *(const uint4*)(lg + i0);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    for (int h = 0; h < kH; ++h) {
+      const int i0 = beg + h * 2048 + threadIdx.x * 8;
+      v[h] = *(const uint4*)(lg + min(i0, a.V - 8));
+    }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint64_t k = vkey(ord16((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), i0 + e);
-          best = k > best ? k : best;
-        }
+    for (int h = 0; h < kH; ++h) {
+      const int i0 = beg + h * 2048 + threadIdx.x * 8;
+      const uint32_t w[4] = {v[h].x, v[h].y, v[h].z, v[h].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint64_t k = vkey(ord16((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), i0 + e);
+        best = (i0 < a.V && k > best) ? k : best;
       }
     }
   } else {
-    for (int i = beg + threadIdx.x; i < min(a.V, beg + kTopChunk); i += blockDim.x) {
+    for (int i = beg + threadIdx.x; i < min(a.V, beg + kArgChunk); i += blockDim.x) {
       const uint64_t k = vkey(ord16(lg[i]), i);
       best = k > best ? k : best;
     }
@@ -753,6 +762,8 @@ namespace {
 constexpr size_t kCntBytes = 160 * kCntStride * sizeof(int);
 
 int nch_top(int V) { return (V + kTopChunk - 1) / kTopChunk; }
+int arg_chunk(int M) { return M <= 8 ? kArgChunkSmall : kArgChunkLarge; }
+int nch_arg(int V, int M) { return (V + arg_chunk(M) - 1) / arg_chunk(M); }  // <= nch_top: fits its workspace
 int nch_run(int V) { return (V + kChunk - 1) / kChunk; }
 
 size_t scratch_bytes(int M, int V) {
@@ -799,7 +810,7 @@ int launch_argmax(const void* logits, int M, int V, int fin, const int64_t* spec
   a.logits = (const uint16_t*)logits;
   a.M = M;
   a.V = V;
-  a.nch = nch_top(V);
+  a.nch = nch_arg(V, M);
   a.fin = fin;
   a.spec = spec;
   a.parent = parent;
@@ -809,7 +820,10 @@ int launch_argmax(const void* logits, int M, int V, int fin, const int64_t* spec
   a.cnt_rows = w.cnt;
   a.cnt_all = w.cnt + 32 * kCntStride;
   a.o = o;
-  hipLaunchKernelGGL(argmax_kernel, dim3(M * a.nch), dim3(256), 0, st, a);
+  if (arg_chunk(M) == kArgChunkSmall)
+    hipLaunchKernelGGL(argmax_kernel<kArgChunkSmall>, dim3(M * a.nch), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(argmax_kernel<kArgChunkLarge>, dim3(M * a.nch), dim3(256), 0, st, a);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
