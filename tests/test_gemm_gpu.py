@@ -96,6 +96,23 @@ def test_strips_per_workgroup_agree(dev, R, M):
     assert torch.equal(y, gfx950.mul(dev_x(x), B, sp, mp))
 
 
+@pytest.mark.parametrize("slots", [2, 3, 5, 12])
+@pytest.mark.parametrize("M", [8, 24])
+def test_slot_counts_in_kernel_sum(dev, slots, M):
+    """Out mode with K slots summed in the kernel by the last-arriving slot: every slot count
+    (odd ones included, which leave the last load step of the slot sum half used) matches the
+    oracle."""
+    from tokenrush_amd import gfx950
+    say(f"slots={slots} M={M}")
+    N, K = 1024, 6144
+    p, s, m = o.make_weights(N, K, seed=7, dtype="fp16")
+    x = o.make_x(M, K, seed=8)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "fp16"))
+    y = gfx950.mul(dev_x(x), B, sp, mp, slots=slots)
+    torch.cuda.synchronize()
+    check_close(y, o.gemm_exact(x, p, s, m), f"slots={slots}")
+
+
 def test_rows_independent_of_m(dev):
     """Row i of an M-row call is bit-identical whatever M is (reference test_marlin.py:42-52)."""
     from tokenrush_amd import gfx950

@@ -52,6 +52,8 @@ constexpr int kSmOff = kQuad * kCodeBytes;        // parameters of the quad's gr
 constexpr int kQuadBytes = kSmOff + 16 * kQuad * 4;  // 4352 = 34 x 128 B
 constexpr int kWsCounterStride = 32;  // ints between workspace counters: one per 128-byte line
                                       // (agent-scope atomics on one line serialize)
+constexpr int kTailE = 4;      // last-arriver slot sum: outputs per thread per pass
+constexpr int kTailS = 2;      // and partial slots loaded per step
 constexpr int kMaxWaves = 12;   // 768 threads: leaves ~170 VGPRs per lane (3 waves per SIMD)
 
 // Groups of a K-long row after padding to whole quads.
@@ -431,25 +433,63 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
            a.S - 1;
   __syncthreads();
   if (!last) return;
-  auto slot_sum = [&](int m, int n) {
-    float v = 0.f;
-    for (int s = 0; s < a.S; ++s)
-      v += __hip_atomic_load(a.ws_part + ((size_t)s * a.M + m) * a.N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return v;
+  // Each thread takes kTailE outputs per pass (two sums each in the pair layout: gate and up)
+  // and loads their partials kTailS slots at a time, all loads of a step issued together at
+  // clamped indices, then adds them in slot order. A loop of dependent loads here waited for
+  // each partial in turn, about 1 us per slot and output.
+  const int F = a.N / 2;
+  const int per_strip = a.silu ? 8 : 16;
+  const int cols = (r1 - r0) * per_strip;
+  const int total = a.M * cols;
+  const size_t slot_stride = (size_t)a.M * a.N;
+  auto col_n = [&](int e, int& m) {  // output e -> row m and the column of its (first) sum
+    m = e / cols;
+    const int c = e % cols;
+    return 16 * phys(r0 + c / per_strip) + c % per_strip;
   };
-  if (a.silu) {
-    const int cols = (r1 - r0) * 8, F = a.N / 2;
-    for (int e = threadIdx.x; e < a.M * cols; e += blockDim.x) {
-      const int m = e / cols, strip = phys(r0 + (e % cols) / 8), j = e % 8;
-      const float g = bf16_bits_to_f32(f32_to_bf16_bits(slot_sum(m, 16 * strip + j)));
-      const float u = bf16_bits_to_f32(f32_to_bf16_bits(slot_sum(m, 16 * strip + j + 8)));
-      ((uint16_t*)a.out)[(size_t)m * F + 8 * strip + j] = f32_to_bf16_bits(silu_mul_f32(g, u));
+  for (int e0 = threadIdx.x; e0 < total; e0 += kTailE * blockDim.x) {
+    size_t off[kTailE];
+    float v[kTailE][2];
+#pragma unroll
+    for (int i = 0; i < kTailE; ++i) {
+      int m;
+      const int n = col_n(min(e0 + i * (int)blockDim.x, total - 1), m);
+      off[i] = (size_t)m * a.N + n;
+      v[i][0] = v[i][1] = 0.f;
     }
-  } else {
-    const int cols = (r1 - r0) * 16;
-    for (int e = threadIdx.x; e < a.M * cols; e += blockDim.x) {
-      const int m = e / cols, n = 16 * phys(r0 + (e % cols) / 16) + e % 16;
-      ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(slot_sum(m, n));
+    for (int s0 = 0; s0 < a.S; s0 += kTailS) {
+      float p[kTailS][kTailE][2];
+#pragma unroll
+      for (int q = 0; q < kTailS; ++q) {
+        const float* base = a.ws_part + (size_t)min(s0 + q, a.S - 1) * slot_stride;
+#pragma unroll
+        for (int i = 0; i < kTailE; ++i) {
+          p[q][i][0] = __hip_atomic_load(base + off[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          p[q][i][1] = a.silu ? __hip_atomic_load(base + off[i] + 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < kTailS; ++q)
+#pragma unroll
+        for (int i = 0; i < kTailE; ++i)
+          if (s0 + q < a.S) {
+            v[i][0] += p[q][i][0];
+            v[i][1] += p[q][i][1];
+          }
+    }
+#pragma unroll
+    for (int i = 0; i < kTailE; ++i) {
+      const int e = e0 + i * (int)blockDim.x;
+      if (e >= total) break;
+      int m;
+      const int n = col_n(e, m);
+      if (a.silu) {
+        const float g = bf16_bits_to_f32(f32_to_bf16_bits(v[i][0]));
+        const float u = bf16_bits_to_f32(f32_to_bf16_bits(v[i][1]));
+        ((uint16_t*)a.out)[(size_t)m * F + (n / 16) * 8 + n % 16] = f32_to_bf16_bits(silu_mul_f32(g, u));
+      } else {
+        ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v[i][0]);
+      }
     }
   }
   if (threadIdx.x == 0)
