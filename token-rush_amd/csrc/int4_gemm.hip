@@ -156,6 +156,31 @@ __device__ __forceinline__ void min_fold(const uint32_t (&sm)[GW], const float (
   for (int mt = 0; mt < MT; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(Xa[mt], c1, acc[mt], 0, 0, 0);
 }
 
+// Output elements of a strip range are numbered e = (s * M + m) * P + j (strip s, row m, column j
+// of P = 8 or 16 per strip row). Thread t takes e = t, t + T, ...: its column j = t % P is fixed,
+// and (m, s) advance by a fixed step, so the index needs one division per kernel instead of
+// several per element (a 32-bit division by a runtime value is ~40 VALU instructions).
+struct StripWalk {
+  int m, s;         // current element's row and strip index
+  int dm, ds;       // step T / P as rows and strips
+  int M;
+  __device__ __forceinline__ StripWalk(int t, int lgP, int T, int M_) : M(M_) {
+    const int q = t >> lgP, dq = T >> lgP;
+    m = q % M_;
+    s = q / M_;
+    dm = dq % M_;
+    ds = dq / M_;
+  }
+  __device__ __forceinline__ void next() {
+    m += dm;
+    s += ds;
+    if (m >= M) {
+      m -= M;
+      ++s;
+    }
+  }
+};
+
 struct GemmArgs {
   const uint16_t* x;      // bf16 [M, K]
   const uint8_t* packed;  // strip layout
@@ -302,6 +327,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     }
   }
   const int slot16 = lane >> 4;
+  const StripWalk walk16(threadIdx.x, 4, blockDim.x, a.M), walk8(threadIdx.x, 3, blockDim.x, a.M);
 
   // Partial tiles of RB consecutive strips are collected in LDS and reduced together (one
   // barrier per batch); batches alternate between two halves of the LDS ring, so the next
@@ -350,18 +376,17 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
           };
           if (a.silu && a.mode == OUT_BF16) {
             // pair layout: rows 0..7 of a strip are gate rows, 8..15 the matching up rows
-            const int per = a.M * 8, F = a.N / 2;
-            for (int e = threadIdx.x; e < ns * per; e += blockDim.x) {
-              const int sidx = e / per, rem = e % per, m = rem >> 3, j = rem & 7;
+            const int F = a.N / 2, j = threadIdx.x & 7;
+            for (StripWalk w = walk8; w.s < ns; w.next()) {
+              const int sidx = w.s, m = w.m;
               const float g = bf16_bits_to_f32(f32_to_bf16_bits(wave_sum(sidx, m, j)));
               const float u = bf16_bits_to_f32(f32_to_bf16_bits(wave_sum(sidx, m, j + 8)));
               ((uint16_t*)a.out)[(size_t)m * F + 8 * phys(r_first + sidx) + j] = f32_to_bf16_bits(silu_mul_f32(g, u));
             }
           } else {
-            const int per = a.M * 16;
-            for (int e = threadIdx.x; e < ns * per; e += blockDim.x) {
-              const int sidx = e / per, rem = e % per;
-              const int m = rem >> 4, n16 = rem & 15;
+            const int n16 = threadIdx.x & 15;
+            for (StripWalk w = walk16; w.s < ns; w.next()) {
+              const int sidx = w.s, m = w.m;
               const float v = wave_sum(sidx, m, n16);
               const int n = 16 * phys(r_first + sidx) + n16;
               if (a.mode == OUT_BF16) {
@@ -434,29 +459,28 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   __syncthreads();
   if (!last) return;
   // Each thread takes kTailE outputs per pass (two sums each in the pair layout: gate and up)
-  // and loads their partials kTailS slots at a time, all loads of a step issued together at
-  // clamped indices, then adds them in slot order. A loop of dependent loads here waited for
-  // each partial in turn, about 1 us per slot and output.
+  // and loads their partials kTailS slots at a time, all loads of a step issued together
+  // (outputs past the range load the last output's partials and store nothing), then adds them
+  // in slot order. A loop of dependent loads here waited for each partial in turn.
   const int F = a.N / 2;
-  const int per_strip = a.silu ? 8 : 16;
-  const int cols = (r1 - r0) * per_strip;
-  const int total = a.M * cols;
+  const int nstr = r1 - r0;
+  const int j = threadIdx.x & (a.silu ? 7 : 15);
   const size_t slot_stride = (size_t)a.M * a.N;
-  auto col_n = [&](int e, int& m) {  // output e -> row m and the column of its (first) sum
-    m = e / cols;
-    const int c = e % cols;
-    return 16 * phys(r0 + c / per_strip) + c % per_strip;
-  };
-  for (int e0 = threadIdx.x; e0 < total; e0 += kTailE * blockDim.x) {
+  for (StripWalk w = a.silu ? walk8 : walk16; w.s < nstr;) {
+    int mi[kTailE], ni[kTailE];
     size_t off[kTailE];
-    float v[kTailE][2];
+    bool live[kTailE];
 #pragma unroll
     for (int i = 0; i < kTailE; ++i) {
-      int m;
-      const int n = col_n(min(e0 + i * (int)blockDim.x, total - 1), m);
-      off[i] = (size_t)m * a.N + n;
-      v[i][0] = v[i][1] = 0.f;
+      live[i] = w.s < nstr;
+      mi[i] = live[i] ? w.m : a.M - 1;
+      ni[i] = 16 * phys(r0 + (live[i] ? w.s : nstr - 1)) + j;
+      off[i] = (size_t)mi[i] * a.N + ni[i];
+      w.next();
     }
+    float v[kTailE][2];
+#pragma unroll
+    for (int i = 0; i < kTailE; ++i) v[i][0] = v[i][1] = 0.f;
     for (int s0 = 0; s0 < a.S; s0 += kTailS) {
       float p[kTailS][kTailE][2];
 #pragma unroll
@@ -479,16 +503,15 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < kTailE; ++i) {
-      const int e = e0 + i * (int)blockDim.x;
-      if (e >= total) break;
-      int m;
-      const int n = col_n(e, m);
+      if (!live[i]) break;
+      const size_t m = mi[i];
+      const int n = ni[i];
       if (a.silu) {
         const float g = bf16_bits_to_f32(f32_to_bf16_bits(v[i][0]));
         const float u = bf16_bits_to_f32(f32_to_bf16_bits(v[i][1]));
-        ((uint16_t*)a.out)[(size_t)m * F + (n / 16) * 8 + n % 16] = f32_to_bf16_bits(silu_mul_f32(g, u));
+        ((uint16_t*)a.out)[m * F + (n >> 4) * 8 + j] = f32_to_bf16_bits(silu_mul_f32(g, u));
       } else {
-        ((uint16_t*)a.out)[(size_t)m * a.N + n] = f32_to_bf16_bits(v[i][0]);
+        ((uint16_t*)a.out)[m * a.N + n] = f32_to_bf16_bits(v[i][0]);
       }
     }
   }
