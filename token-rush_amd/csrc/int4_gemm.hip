@@ -691,13 +691,18 @@ template <int MT, int GW, bool F16S, bool XDMA>
 hipError_t launch_t(GemmArgs a, const Plan& p, hipStream_t stream) {
   const dim3 grid(p.grid_n * p.S), block(64 * p.W);
   const size_t per_strip = (size_t)p.W * MT * 256 * sizeof(float);
-  int rb = (int)(kLdsBudget / (2 * per_strip));
+  // Ring budget: the staged kernel keeps 64 KB (its staging takes the rest); the others share
+  // the CU's LDS among the workgroups the plan puts on one CU, so larger batches never cost
+  // occupancy.
+  const int wg_per_cu = p.W >= kWavesPerCU ? 1 : kWavesPerCU / p.W;
+  int rb = (int)((XDMA ? kLdsBudget : kLdsMax / wg_per_cu) / (2 * per_strip));
   a.RB = rb < 1 ? 1 : (rb > 4 ? 4 : rb);
   const size_t ring = 2 * a.RB * per_strip;
   a.xstage_off = (int)ring;
   const size_t lds = XDMA ? ring + (size_t)p.W * GW * 2048 : ring;
-  if (XDMA) {
-    // staging + ring exceed the default 64 KB of dynamic LDS: raise this kernel's limit once
+  {
+    // staging + ring, or a ring over 64 KB, exceed the default 64 KB of dynamic LDS: raise this
+    // kernel's limit once
     static bool raised = false;
     if (!raised) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&int4_gemm_kernel<MT, GW, F16S, XDMA>),
