@@ -197,6 +197,34 @@ def test_accept_tree_config4(dev, seed):
     assert ref["n"] >= depth[node]
 
 
+@pytest.mark.parametrize("M", [1, 2, 5, 17, 32])
+@pytest.mark.parametrize("shape", ["chain", "star", "random"])
+def test_accept_tree_shapes(dev, M, shape):
+    """Tree accept over shapes the config-4 trees do not reach: a chain M - 1 deep (all
+    accepted, and cut at a random node), a star (depth-1 ties: the lowest index wins) and random
+    trees where most nodes are accepted (many equal-depth accepted leaves)."""
+    from tokenrush_amd.accept import accept_tree
+    V = 4096
+    rng = np.random.default_rng(1000 * M + len(shape))
+    for trial in range(6):
+        say(f"tree {shape} M={M} trial={trial}")
+        if shape == "chain":
+            parent = np.arange(-1, M - 1, dtype=np.int64)
+        elif shape == "star":
+            parent = np.array([-1] + [0] * (M - 1), dtype=np.int64)
+        else:
+            parent = np.array([-1] + [int(rng.integers(0, i)) for i in range(1, M)], dtype=np.int64)
+        lg = oa.planted_logits(M, V, seed=2000 + 10 * M + trial)
+        pred = oa.argmax_rows(lg)
+        toks = rng.integers(0, V, M).astype(np.int64)
+        for i in range(1, M):  # accept most nodes: node i's token is its parent's prediction
+            if rng.random() < (0.9 if trial % 2 == 0 else 0.6):
+                toks[i] = pred[parent[i]]
+        st = state(M, pos=7 + trial)
+        accept_tree(dev_logits(lg), torch.from_numpy(toks).to(dev), torch.from_numpy(parent.astype(np.int32)).to(dev), st)
+        check_state(st, oa.tree_accept(pred, toks, parent, pos=7 + trial), M)
+
+
 def test_commit_rows_tree(dev):
     """Tree commit moves the accepted path's rows to consecutive positions in every plane."""
     from tokenrush_amd.accept import accept_tree, commit_rows

@@ -419,11 +419,10 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
     if (a.fin == FIN_TREE) parent[threadIdx.x] = a.parent[threadIdx.x];
   }
   ws_gather(a.preds, a.M, pred);
-  if (threadIdx.x == 0) {
-    if (a.fin == FIN_CHAIN)
-      finish_chain(pred, spec, a.M, a.o);
-    else
-      finish_tree(pred, spec, parent, a.M, a.o);
+  if (a.fin == FIN_CHAIN) {
+    if (threadIdx.x == 0) finish_chain(pred, spec, a.M, a.o);
+  } else if (threadIdx.x < 64) {
+    finish_tree(pred, spec, parent, a.M, a.o);
   }
 }
 

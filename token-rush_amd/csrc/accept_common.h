@@ -108,36 +108,61 @@ static __device__ __forceinline__ void finish_chain(const int64_t* pred, const i
 
 // Longest accepted root path of a draft tree (bench/tree_accept.py:91-100): node 0 is the
 // root; node i > 0 (parent[i] < i) is accepted when its token equals the prediction of its
-// parent's row and the parent is accepted. Deepest accepted node wins, lowest index on ties.
-// Runs on one thread with its node arrays in LDS (no scratch, no registers held by the
-// chunk-scanning part of the kernel).
+// parent's row and the parent is accepted. Deepest accepted node wins, lowest index on ties. A
+// node with a malformed parent (not in 0..i-1) is not accepted, has depth 0, and nothing below
+// it is accepted.
+//
+// Called by all 64 lanes of one wave, lane i = node i (M <= 32). Depth and acceptance come from
+// pointer jumping: each lane holds (up, dep, ok) = an ancestor, the edge count to it and the AND
+// of the edge checks on the way, and five rounds of "combine with up's triple" reach the root
+// (or the malformed node) from depth <= 31. A one-thread walk over the nodes in index order took
+// several microseconds of dependent LDS accesses at M = 32.
 static __device__ void finish_tree(const int64_t* pred, const int64_t* node_tok, const int32_t* parent, int M,
-                                         const AcceptOut& o) {
-  __shared__ int ok[32], depth[32], path[32];
-  ok[0] = 1;
-  depth[0] = 0;
-  int best = 0;
-  for (int i = 1; i < M; ++i) {
-    const int p = parent[i];
-    const bool valid = p >= 0 && p < i;  // a malformed parent array accepts nothing below it
-    depth[i] = valid ? depth[p] + 1 : 0;
-    ok[i] = valid && ok[p] && node_tok[i] == pred[p];
-    if (ok[i] && depth[i] > depth[best]) best = i;
+                                   const AcceptOut& o) {
+  const int i = threadIdx.x & 63;
+  const bool node = i < M;
+  const int p = node && i > 0 ? parent[i] : -1;
+  const bool valid = node && i > 0 && p >= 0 && p < i;
+  int up = valid ? p : -1;
+  int dep = valid ? 1 : 0;
+  int ok = i == 0 ? 1 : (valid && node_tok[i] == pred[p]) ? 1 : 0;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    const int src = up < 0 ? i : up;
+    const int up2 = __shfl(up, src), dep2 = __shfl(dep, src), ok2 = __shfl(ok, src);
+    if (up >= 0) {
+      ok &= ok2;
+      dep += dep2;
+      up = up2;
+    }
   }
-  const int n = depth[best];
-  for (int j = best, d = n; d >= 0; --d) {
-    path[d] = j;
-    j = d > 0 ? parent[j] : 0;
+  // deepest accepted node, lowest index on ties: max of (depth, 63 - index)
+  uint32_t key = node && ok ? ((uint32_t)dep << 8) | (uint32_t)(63 - i) : 0u;
+  key = max(key, xor_lane<1>(key));
+  key = max(key, xor_lane<2>(key));
+  key = max(key, xor_lane<4>(key));
+  key = max(key, xor_lane<8>(key));
+  key = max(key, xor_lane<16>(key));
+  key = max(key, xor_lane<32>(key));
+  const int best = 63 - (int)(key & 0xFFu), n = (int)(key >> 8);
+  // path[d] (the ancestor of best at depth d) in lane d, walking up from best
+  int path = -1;
+  for (int d = n, j = best; d >= 0; --d) {
+    if (i == d) path = j;
+    j = __shfl(p, j);
   }
-  const int64_t base = *o.pos;
+  const int next = __shfl(path, (i + 1) & 63);  // path[i + 1]
   const int64_t t = pred[best];
-  *o.n_accepted = n;
-  *o.tok = t;
-  *o.pos = base + n + 1;
-  *o.slot = best;
-  for (int i = 0; i < M; ++i) {
-    o.tokens[i] = i < n ? node_tok[path[i + 1]] : (i == n ? t : -1);
-    o.commit[i] = i <= n ? path[i] : -1;
+  const int64_t base = *o.pos;
+  if (node) {
+    o.tokens[i] = i < n ? node_tok[next] : (i == n ? t : -1);
+    o.commit[i] = i <= n ? path : -1;
+  }
+  if (i == 0) {
+    *o.n_accepted = n;
+    *o.tok = t;
+    *o.pos = base + n + 1;
+    *o.slot = best;
   }
 }
 
