@@ -420,7 +420,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
   }
   ws_gather(a.preds, a.M, pred);
   if (a.fin == FIN_CHAIN) {
-    if (threadIdx.x == 0) finish_chain(pred, spec, a.M, a.o);
+    if (threadIdx.x < 64) finish_chain(pred, spec, a.M, a.o);
   } else if (threadIdx.x < 64) {
     finish_tree(pred, spec, parent, a.M, a.o);
   }
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   if (threadIdx.x < a.M) spec[threadIdx.x] = a.spec[threadIdx.x];
   ws_gather(a.preds, a.M, pred);
   if (a.o.pred && threadIdx.x < a.M) a.o.pred[threadIdx.x] = pred[threadIdx.x];
-  if (threadIdx.x == 0) finish_chain(pred, spec, a.M, a.o);
+  if (threadIdx.x < 64) finish_chain(pred, spec, a.M, a.o);
 }
 
 // ------------------------------------------------------------------ residual rejection sampling
@@ -705,16 +705,19 @@ __global__ __launch_bounds__(64) void residual_phase3_kernel(ResidualArgs a) {
     }
     pick = (int)vkey_idx(wave_max_u64(b));
   }
-  if (lane == 0) {
+  {
+    // lane i writes output i (a one-lane loop waited for each draft token load in turn)
     const int n = j;  // drafts a.spec[1..n] were accepted
     const int64_t base = *a.o.pos;
-    *a.o.n_accepted = n;
-    *a.o.tok = pick;
-    *a.o.pos = base + n + 1;
-    *a.o.slot = n;
-    for (int i = 0; i < a.M; ++i) {
-      a.o.tokens[i] = i < n ? a.spec[i + 1] : (i == n ? pick : -1);
-      a.o.commit[i] = i <= n ? base + i : -1;
+    if (lane < a.M) {
+      a.o.tokens[lane] = lane < n ? a.spec[lane + 1] : (lane == n ? pick : -1);
+      a.o.commit[lane] = lane <= n ? base + lane : -1;
+    }
+    if (lane == 0) {
+      *a.o.n_accepted = n;
+      *a.o.tok = pick;
+      *a.o.pos = base + n + 1;
+      *a.o.slot = n;
     }
   }
 }

@@ -92,17 +92,22 @@ struct AcceptOut {
 // Engine._verify_step (tokenrush/model.py:302-312): match = pred[:K] == spec[1:M],
 // n = leading matches, tok = pred[n], pos += n + 1, slot = n.
 static __device__ __forceinline__ void finish_chain(const int64_t* pred, const int64_t* spec, int M, const AcceptOut& o) {
-  int n = 0;
-  while (n < M - 1 && pred[n] == spec[n + 1]) ++n;
-  const int64_t base = *o.pos;
+  // Called by all 64 lanes of one wave: lane i checks draft i + 1 against row i's prediction,
+  // n = the first mismatch (a ballot), and lane i writes output i.
+  const int i = threadIdx.x & 63;
+  const bool miss = i >= M - 1 || pred[i] != spec[i + 1];
+  const int n = __builtin_ctzll(__ballot(miss));  // lane M - 1 always misses
   const int64_t t = pred[n];
-  *o.n_accepted = n;
-  *o.tok = t;
-  *o.pos = base + n + 1;
-  *o.slot = n;
-  for (int i = 0; i < M; ++i) {
+  const int64_t base = *o.pos;
+  if (i < M) {
     o.tokens[i] = i < n ? spec[i + 1] : (i == n ? t : -1);
     o.commit[i] = i <= n ? base + i : -1;
+  }
+  if (i == 0) {
+    *o.n_accepted = n;
+    *o.tok = t;
+    *o.pos = base + n + 1;
+    *o.slot = n;
   }
 }
 

@@ -442,7 +442,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     }
     if (a.spec && threadIdx.x < a.M) spec[threadIdx.x] = a.spec[threadIdx.x];
     __syncthreads();
-    if (a.spec && threadIdx.x == 0) finish_chain(pred, spec, a.M, a.o);
+    if (a.spec && threadIdx.x < 64) finish_chain(pred, spec, a.M, a.o);
     return;
   }
   if (a.mode != OUT_BF16_VIA_WS) return;
