@@ -39,11 +39,12 @@ namespace tr {
 
 constexpr int kGdnK = 128;   // key head dim
 constexpr int kGdnV = 128;   // value head dim
-constexpr int kGdnBV = 32;   // value columns per step workgroup
+constexpr int kGdnBV = 16;   // value columns per step workgroup: 2 per lane (8 column pairs x 8 row groups)
 constexpr int kGdnNVB = kGdnV / kGdnBV;
 constexpr int kGdnMaxM = 8;  // tokens per step (the reference's MP, fused.py:150)
 constexpr int kGdnThreads = 256;
-static_assert(kGdnMaxM * kGdnBV == kGdnThreads, "one v element per thread in the step prologue");
+static_assert(kGdnMaxM * kGdnBV <= kGdnThreads, "at most one v element per thread in the step prologue");
+static_assert(kGdnBV == 16, "the step kernel's lane layout: 8 column pairs");
 
 struct GdnArgs {
   const uint16_t* qkvz;    // [M, ld] bf16: q | k | v | z
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
 __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   __shared__ float cq[kGdnMaxM][kGdnK], ck[kGdnMaxM][kGdnK], cv[kGdnMaxM][kGdnBV];
   __shared__ float beta_s[kGdnMaxM], decay_s[kGdnMaxM];
-  __shared__ float4 red[2][4][8], red_n[2][4][8];
+  __shared__ float2 red[2][4][8], red_n[2][4][8];
   __shared__ int last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hv = blockIdx.x / kGdnNVB, vb = blockIdx.x % kGdnNVB;
@@ -201,16 +202,16 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   const int QK = a.H * kGdnK, VAL = a.HV * kGdnV;
   const int64_t slot = *a.slot;
   const int vq = lane & 7, kg = lane >> 3;
-  const int c0 = 4 * vq;                    // this lane's first column within the block
+  const int c0 = 2 * vq;                    // this lane's first column within the block
   const int v0 = vb * kGdnBV + c0;          // ... within the head
   const int k0 = 32 * wave + 4 * kg;        // this lane's first row
 
   // prologue: the committed state tile, then this block's normalised q / k, v and gates
-  float4 S[4];
+  float2 S[4];
   {
     const float* src = a.rec + slot * a.slot_stride + (size_t)hv * kGdnK * kGdnV + v0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) S[j] = *(const float4*)(src + (size_t)(k0 + j) * kGdnV);
+    for (int j = 0; j < 4; ++j) S[j] = *(const float2*)(src + (size_t)(k0 + j) * kGdnV);
   }
   // q / k, v and the gates: every load issued at once (a loop with a runtime bound waited for
   // each iteration's loads); indices past M are clamped to token M - 1 and not stored
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
       qv[q] = a.qk[(size_t)t * 2 * QK + ih * kGdnK + c];
       kv2[q] = a.qk[(size_t)t * 2 * QK + QK + ih * kGdnK + c];
     }
-    const int ev = tid, tv = min(ev / kGdnBV, M - 1), cvi = ev % kGdnBV;  // kGdnMaxM * kGdnBV == kGdnThreads
+    const int ev = min(tid, kGdnMaxM * kGdnBV - 1), tv = min(ev / kGdnBV, M - 1), cvi = ev % kGdnBV;
     const uint16_t vraw = a.vconv[(size_t)tv * VAL + hv * kGdnV + vb * kGdnBV + cvi];
     const int tg = min(tid, M - 1);
     const float b = a.gates[(size_t)tg * 2 * a.HV + hv];
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
         ck[t][c] = kv2[q];
       }
     }
-    if (ev / kGdnBV < M) cv[ev / kGdnBV][cvi] = bf16_bits_to_f32(vraw);
+    if (tid < kGdnMaxM * kGdnBV && ev / kGdnBV < M) cv[ev / kGdnBV][cvi] = bf16_bits_to_f32(vraw);
     if (tid < M) {
       beta_s[tid] = bf16r(1.f / (1.f + expf(-b)));
       decay_s[tid] = expf(a.A[hv] * softplus_f(av + a.dt_bias[hv]));
@@ -249,31 +250,27 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   // and kv_{t+1} is summed together with o_t, so each token costs one cross-wave exchange.
   // Sums over k: a lane's 4 rows, the wave's 8 row groups (lane ^ 8, ^ 16, ^ 32), the 4 waves.
   auto ksum = [](float v) { return sum_x32(sum_x16(sum_x8(v))); };
-  auto wsum = [&](float4 p, int buf) {  // every lane of every wave must call it
-    p = make_float4(ksum(p.x), ksum(p.y), ksum(p.z), ksum(p.w));
+  auto wsum = [&](float2 p, int buf) {  // every lane of every wave must call it
+    p = make_float2(ksum(p.x), ksum(p.y));
     if (kg == 0) red[buf][wave][vq] = p;
     __syncthreads();
-    float4 r = red[buf][0][vq];
+    float2 r = red[buf][0][vq];
 #pragma unroll
     for (int w = 1; w < 4; ++w) {
-      const float4 u = red[buf][w][vq];
+      const float2 u = red[buf][w][vq];
       r.x += u.x;
       r.y += u.y;
-      r.z += u.z;
-      r.w += u.w;
     }
     return r;
   };
-  float4 kv;
+  float2 kv;
   {
-    float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 p = make_float2(0.f, 0.f);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float kk = ck[0][k0 + j];
       p.x += S[j].x * kk;
       p.y += S[j].y * kk;
-      p.z += S[j].z * kk;
-      p.w += S[j].w * kk;
     }
     kv = wsum(p, 0);
   }
@@ -281,61 +278,47 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   for (int t = 0; t < M; ++t) {
     const float beta = beta_s[t], eg = decay_s[t];
     const float* vt = &cv[t][c0];
-    float4 dv;
+    float2 dv;
     dv.x = beta * (vt[0] - eg * kv.x);
     dv.y = beta * (vt[1] - eg * kv.y);
-    dv.z = beta * (vt[2] - eg * kv.z);
-    dv.w = beta * (vt[3] - eg * kv.w);
     const bool more = t + 1 < M;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f), nx = o;
+    float2 o = make_float2(0.f, 0.f), nx = o;
     float* dst = a.rec + (size_t)t * a.slot_stride + (size_t)hv * kGdnK * kGdnV + v0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float kk = ck[t][k0 + j], qq = cq[t][k0 + j], kn = more ? ck[t + 1][k0 + j] : 0.f;
       S[j].x = S[j].x * eg + kk * dv.x;
       S[j].y = S[j].y * eg + kk * dv.y;
-      S[j].z = S[j].z * eg + kk * dv.z;
-      S[j].w = S[j].w * eg + kk * dv.w;
-      *(float4*)(dst + (size_t)(k0 + j) * kGdnV) = S[j];
+      *(float2*)(dst + (size_t)(k0 + j) * kGdnV) = S[j];
       o.x += S[j].x * qq;
       o.y += S[j].y * qq;
-      o.z += S[j].z * qq;
-      o.w += S[j].w * qq;
       nx.x += S[j].x * kn;
       nx.y += S[j].y * kn;
-      nx.z += S[j].z * kn;
-      nx.w += S[j].w * kn;
     }
     // both sums in one exchange: buffer (t + 1) % 2 alternates so the next token's writes never
     // race this token's reads (the barrier inside wsum separates them)
-    o = make_float4(ksum(o.x), ksum(o.y), ksum(o.z), ksum(o.w));
-    nx = make_float4(ksum(nx.x), ksum(nx.y), ksum(nx.z), ksum(nx.w));
+    o = make_float2(ksum(o.x), ksum(o.y));
+    nx = make_float2(ksum(nx.x), ksum(nx.y));
     const int buf = (t + 1) & 1;
     if (kg == 0) {
       red[buf][wave][vq] = o;
       red_n[buf][wave][vq] = nx;
     }
     __syncthreads();
-    float4 ro = red[buf][0][vq], rn = red_n[buf][0][vq];
+    float2 ro = red[buf][0][vq], rn = red_n[buf][0][vq];
 #pragma unroll
     for (int w = 1; w < 4; ++w) {
-      const float4 u = red[buf][w][vq], q2 = red_n[buf][w][vq];
+      const float2 u = red[buf][w][vq], q2 = red_n[buf][w][vq];
       ro.x += u.x;
       ro.y += u.y;
-      ro.z += u.z;
-      ro.w += u.w;
       rn.x += q2.x;
       rn.y += q2.y;
-      rn.z += q2.z;
-      rn.w += q2.w;
     }
     kv = rn;
     if (wave == 0 && kg == 0) {
       float* op = obase + (size_t)t * VAL;
       ws_st(op + 0, bf16r(ro.x));
       ws_st(op + 1, bf16r(ro.y));
-      ws_st(op + 2, bf16r(ro.z));
-      ws_st(op + 3, bf16r(ro.w));
     }
   }
 
