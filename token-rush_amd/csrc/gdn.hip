@@ -281,12 +281,12 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
     float2 dv;
     dv.x = beta * (vt[0] - eg * kv.x);
     dv.y = beta * (vt[1] - eg * kv.y);
-    const bool more = t + 1 < M;
+    const int tn = min(t + 1, M - 1);  // the next token's k (the last token's sum is unused)
     float2 o = make_float2(0.f, 0.f), nx = o;
     float* dst = a.rec + (size_t)t * a.slot_stride + (size_t)hv * kGdnK * kGdnV + v0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float kk = ck[t][k0 + j], qq = cq[t][k0 + j], kn = more ? ck[t + 1][k0 + j] : 0.f;
+      const float kk = ck[t][k0 + j], qq = cq[t][k0 + j], kn = ck[tn][k0 + j];
       S[j].x = S[j].x * eg + kk * dv.x;
       S[j].y = S[j].y * eg + kk * dv.y;
       *(float2*)(dst + (size_t)(k0 + j) * kGdnV) = S[j];
