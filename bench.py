@@ -15,6 +15,8 @@ value       whole-job algorithmic bytes / wall time of the timed steps (GB/s); b
 roofline    the dominant kernel (gate/up, 53% of the bytes): its algorithmic bytes / its mean
             duration, measured with HIP events around a graph of back-to-back launches of that
             kernel alone over all weight copies, on the launch stream; vs 8 TB/s.
+config1     benchmark config 1: a single 5120x5120 GEMV at M = 1 over >= 1 GiB of weight copies,
+            mean us per launch, GB/s and % of 8 TB/s.
 accept      on-device accept latency (benchmark config 3 and 4): mean per launch over a graph of
             back-to-back calls.
 config5     one verify step of the random-init 64-layer hybrid at M = 8 (257 int4 GEMMs, split-K
@@ -112,6 +114,33 @@ def kernel_means(torch, gfx950, copies, xs, reps=4):
     return out
 
 
+def config1_gemv(torch, gfx950, dev, reps=4):
+    """benchmark config 1: one 5120x5120 int4 g128 GEMV at M = 1 (fp16 scale/min, x ~ N(0, 1)),
+    cycled over >= 1 GiB of distinct weight copies so every launch reads HBM: mean microseconds per
+    launch over a graph of back-to-back launches, GB/s of its algorithmic bytes, % of 8 TB/s."""
+    N = K = 5120
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(101)
+    per = N * K // 2 + 4 * N * K // 128
+    n_copies = -(-(1 << 30) // per)
+    ws = []
+    for _ in range(n_copies):
+        q = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=gen)
+        s = (torch.rand(N, K // 128, device=dev, generator=gen) * 0.018 + 0.002).half()
+        m = (torch.rand(N, K // 128, device=dev, generator=gen) * 0.14 - 0.15).half()
+        B, sv, _ = gfx950.pack(q, s, m)
+        ws.append((B, sv))
+    x = torch.randn(1, K, device=dev, generator=gen).to(torch.bfloat16)
+    g = graph_of(torch, lambda: [gfx950.mul(x, B, sv) for _ in range(reps) for B, sv in ws])
+    t = timed_graph(torch, g) / (reps * n_copies)
+    del g, ws
+    nbytes = algo_bytes(N, K, 1)
+    return {"us": round(t * 1e6, 3), "GBps": round(nbytes / t / 1e9, 1),
+            "pct_of_hbm_peak": round(100 * nbytes / t / 1e9 / HBM_PEAK_GBS, 2), "bytes": nbytes,
+            "copies": n_copies, "note": "5120x5120 M=1 fp16 scale/min; mean per launch over a graph of "
+                                        "%d back-to-back launches (launch gap included)" % (reps * n_copies)}
+
+
 def accept_latency(torch, dev):
     """Mean microseconds per launch of the accept kernels at benchmark configs 3 and 4."""
     from tokenrush_amd.accept import AcceptState, accept_greedy, accept_residual, accept_sampled, accept_tree
@@ -161,6 +190,9 @@ def config5_step(torch, dev, M=M_VERIFY, reps=10):
     st.slot.zero_()
     g = graph_of(torch, lambda: model.step(x0, spec, st))
     build_s = time.perf_counter() - t0
+    # each replay advances pos by at most M: the replays below stay inside the cache's headroom
+    assert (reps + 3) * M <= model.cfg.headroom
+    st.pos.fill_(model.cfg.live)
     t = timed_graph(torch, g, reps=reps)
     nbytes, state_bytes, live = model.nbytes(), model.state.nbytes(), model.cfg.live
     n_attn = sum(1 for li in range(model.cfg.n_layers) if model.cfg.is_attention(li))
@@ -216,7 +248,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer verify-step graph (config 5)")
-    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5"],
+    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config1"],
                     help="profiling aid: run just this projection's launches (M=8), or the config-5 step graph, and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: run a plain 1 GiB device copy (read 1 GiB, write 1 GiB) and exit")
@@ -237,6 +269,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
+    if a.only == "config1":
+        print(json.dumps({"config1_gemv_m1": config1_gemv(torch, gfx950, dev)}))
         return
     if a.only == "config5":
         print(json.dumps({"config5_verify_step": config5_step(torch, dev, reps=max(1, a.steps // 30))}))
@@ -271,6 +306,8 @@ def main():
         sweep[M] = round(sum(kernel_means(torch, gfx950, copies, xsM, reps=2).values()) * 1e6, 2)
     acc = accept_latency(torch, dev)
     del copies
+    torch.cuda.empty_cache()
+    c1 = config1_gemv(torch, gfx950, dev)
     torch.cuda.empty_cache()
     c5 = None if a.no_config5 else config5_step(torch, dev)
 
@@ -308,6 +345,7 @@ def main():
                              "sampled_m8": round(sum(k8.values()) * 1e6 + acc["sampled_m8"], 2),
                              "residual_m8": round(sum(k8.values()) * 1e6 + acc["residual_m8"], 2),
                              "tree_m32": round(sweep.get(32, float("nan")) + acc["tree_m32"], 2)},
+        "config1_gemv_m1": c1,
         "config5_verify_step": c5,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -170,9 +170,11 @@ int tr_accept_tree(const void* logits, int M, int V, const int64_t* node_toks, c
 /* Tree commit of a cache laid out [planes][max_len][row_bytes]: row (pos - n - 1) + commit[t]
  * moves to row (pos - n - 1) + t for t = 1..n, reading n and pos after the accept. For the
  * reference's KV cache and its scales (tokenrush/state.py:19-29), whose chain commit is only
- * the position advance (model.py:376-382). */
+ * the position advance (model.py:376-382). A commit that would reach rows outside the cache or
+ * move more than max_n (<= 32) rows moves nothing and sets *status to 1 (status: device int32,
+ * may be null; never cleared by the call). */
 int tr_commit_rows(void* data, int planes, long plane_stride_bytes, int row_bytes, const int64_t* pos,
-                   const int64_t* n_accepted, const int64_t* commit, int max_n, void* stream);
+                   const int64_t* n_accepted, const int64_t* commit, int max_n, int32_t* status, void* stream);
 
 /* ---------------------------------------------------------------- row kernels around the GEMMs */
 
@@ -204,7 +206,7 @@ size_t tr_gdn_workspace_bytes(int M, int H, int HV);
  *   A and dt_bias [HV] fp32, rec fp32 slots slot_stride floats apart, each [HV, K, V]; the committed
  *   state is slot *slot (device int64); pos: device int64 position of token 0; norm_w [V] bf16;
  *   y [M, HV V] bf16. K == V == 128, HV % H == 0, R >= M + 3, hidden % 32 == 0. Two launches: the
- *   conv + gates of all heads, then the recurrence per (value head, 32-column block).
+ *   conv + gates of all heads, then the recurrence per (value head, 16-column block): HV x 8 workgroups.
  * Replaces: gdn_step_fused (tokenrush/fused.py:119-236: _gdn_step_fused_kernel + _gated_norm_kernel),
  * the fused path of gdn_forward (tokenrush/model.py:76-80). */
 int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void* ring, const void* conv_w,

@@ -240,9 +240,11 @@ def test_commit_rows_tree(dev):
     sc = torch.rand(4, 2, 64, device=dev)                                          # per-(head, pos) scale
     kv0, sc0 = kv.clone(), sc.clone()
     accept_tree(dev_logits(lg), torch.from_numpy(toks).to(dev), torch.from_numpy(parent).to(dev), st)
-    commit_rows(kv, st)
-    commit_rows(sc, st)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    commit_rows(kv, st, "rows", status=status)
+    commit_rows(sc, st, "scalars", status=status)
     torch.cuda.synchronize()
+    assert int(status) == 0
     ref = oa.tree_accept(oa.argmax_rows(lg), toks, parent, pos=20)
     assert ref["commit"] == [0, 1, 3, 5]
     exp_kv, exp_sc = kv0.clone(), sc0.clone()
@@ -250,6 +252,22 @@ def test_commit_rows_tree(dev):
         exp_kv[:, :, 20 + t] = kv0[:, :, 20 + node]
         exp_sc[:, :, 20 + t] = sc0[:, :, 20 + node]
     assert torch.equal(kv, exp_kv) and torch.equal(sc, exp_sc)
+    # a per-layer cache [kv_heads, max_len, head_dim] (one StepState.k[a]) commits the same way
+    one = kv0[1].clone()
+    commit_rows(one, st, "rows", status=status)
+    torch.cuda.synchronize()
+    assert torch.equal(one, exp_kv[1]) and int(status) == 0
+    # more rows than max_n, or rows past the cache's end: nothing moves and status reads 1
+    before = kv.clone()
+    commit_rows(kv, st, "rows", max_n=2, status=status)
+    torch.cuda.synchronize()
+    assert int(status) == 1 and torch.equal(kv, before)
+    status.zero_()
+    short = kv0[:, :, :22].contiguous()                  # max_len 22: rows 20 + 5 are outside
+    short0 = short.clone()
+    commit_rows(short, st, "rows", status=status)
+    torch.cuda.synchronize()
+    assert int(status) == 1 and torch.equal(short, short0)
 
 
 def test_accept_in_graph_replays(dev):

@@ -145,3 +145,41 @@ def test_attn_graph_replay(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y_g, y_eager)
+
+
+def test_positions_past_the_cache_write_nothing_outside(dev):
+    """A device position with pos + M beyond the cache (maxlen rows): the prep writes rows
+    pos..maxlen-1 only and leaves every other row of the allocation alone (the next kv head's
+    first rows, where an unguarded write of head j's row maxlen would land), and decode reads
+    at most maxlen rows."""
+    print("attn past the cache", flush=True)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    M, maxlen = 6, 64
+    pos = maxlen - 2                                   # tokens 2..5 fall outside the cache
+    qkv = torch.randn(M, QKV, device=dev, generator=gen).to(torch.bfloat16)
+    qw = (torch.randn(D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    kw = (torch.randn(D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    cos, sin = rope_table(maxlen, RD, CFG.rope_theta, dev)
+    kc, vc, ks, vs = _filled_cache(gen, dev, maxlen, maxlen - 2)
+    before = [t.clone() for t in (kc, vc, ks, vs)]
+    pos_t = torch.tensor([pos], device=dev)
+    q = attn_prep(qkv, qw, kw, cos, sin, pos_t, kc, vc, CFG, ks, vs)
+    out = attn_decode_fused(q, qkv, kc, vc, pos_t, CFG, ks, vs)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    for t, t0 in zip((kc, vc), before[:2]):
+        assert torch.equal(t[:, :pos].view(torch.uint8), t0[:, :pos].view(torch.uint8))
+        assert not torch.equal(t[:, pos:].view(torch.uint8), t0[:, pos:].view(torch.uint8))
+    for t, t0 in zip((ks, vs), before[2:]):
+        assert torch.equal(t[:, :pos], t0[:, :pos])
+    # the two in-cache tokens match a call whose cache is long enough for all six
+    big = maxlen + 8
+    cos2, sin2 = rope_table(big, RD, CFG.rope_theta, dev)
+    kc2 = torch.zeros(HKV, big, D, device=dev, dtype=F8)
+    vc2 = torch.zeros_like(kc2)
+    ks2, vs2 = torch.ones(HKV, big, device=dev), torch.ones(HKV, big, device=dev)
+    attn_prep(qkv, qw, kw, cos2, sin2, pos_t, kc2, vc2, CFG, ks2, vs2)
+    torch.cuda.synchronize()
+    assert torch.equal(kc[:, pos:].view(torch.uint8), kc2[:, pos:maxlen].view(torch.uint8))
+    assert torch.equal(ks[:, pos:], ks2[:, pos:maxlen])

@@ -51,3 +51,71 @@ def test_missing_shards_and_matrix(tmp_path):
         ck.read_tensors(str(tmp_path))
     with pytest.raises(RuntimeError):
         ck.linear({}, "lm_head.weight", "cpu")
+
+
+class _FakeLinear:
+    """CPU stand-in for a QLinear: nibbles() returns an engine-packed triple of the given shape."""
+
+    def __init__(self, N, K):
+        self.t = (torch.zeros(N, K // 2, dtype=torch.uint8), torch.ones(N, K // 128, dtype=torch.bfloat16),
+                  torch.zeros(N, K // 128, dtype=torch.bfloat16))
+
+    def nibbles(self):
+        return self.t
+
+
+def _fake_model(cfg):
+    """An object with the attributes checkpoint.model_items reads, on the CPU."""
+    from types import SimpleNamespace as NS
+    H, z = cfg.hidden, lambda *s: torch.zeros(*s, dtype=torch.bfloat16)
+    layers = []
+    for li in range(cfg.n_layers):
+        L = NS(attention=cfg.is_attention(li), ln1=z(H), ln2=z(H), gate_up=_FakeLinear(2 * cfg.mlp, H),
+               down=_FakeLinear(H, cfg.mlp))
+        if L.attention:
+            L.split = (cfg.n_heads * 2 * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim)
+            L.proj, L.out = _FakeLinear(cfg.attn_qkv, H), _FakeLinear(H, cfg.attn_out)
+            L.q_norm_w, L.k_norm_w = z(cfg.head_dim), z(cfg.head_dim)
+        else:
+            g = cfg.gdn
+            L.split = (g.conv_dim,)
+            L.proj, L.out = _FakeLinear(cfg.gdn_in, H), _FakeLinear(H, cfg.gdn_out)
+            L.in_ba, L.conv_w, L.norm_w = z(2 * g.gdn_v_heads, H), z(g.conv_dim, 4), z(g.gdn_v_dim)
+            L.A_log, L.A, L.dt_bias = (torch.zeros(g.gdn_v_heads) for _ in range(3))
+        layers.append(L)
+    return NS(layers=layers, final_norm=z(H), lm_head=_FakeLinear(cfg.vocab, H), embed=z(cfg.vocab, H), cfg=cfg)
+
+
+def test_saved_names_cover_the_reference_loader(tmp_path):
+    """A saved model holds every name the reference's build_weights reads (weights.py:180-211),
+    embed_tokens.weight included, and nothing outside that set; the quantized matrices are
+    exactly the projections and the lm_head."""
+    m = _fake_model(SMALL)
+    items = ck.model_items(m)
+    names = [n for n, _ in items]
+    assert set(names) == ck.required_names(SMALL) and len(names) == len(set(names))
+    info = ck.write_packed(str(tmp_path), items, SMALL, shard_bytes=1 << 20)
+    assert set(info["quantized"]) == {n for n in names if "_proj" in n and not n.endswith(("_a.weight", "_b.weight"))} | {"lm_head.weight"}
+    t = ck.read_tensors(str(tmp_path))
+    stored = {n[:-len(suf)] for n in t for suf in (".qweight",) if n.endswith(suf)} | {
+        n for n in t if not n.endswith((".qweight", ".scale", ".mn"))}
+    assert stored == ck.required_names(SMALL)
+    assert t["layers.0.linear_attn.conv1d.weight"].shape == (SMALL.gdn.conv_dim, 1, 4)   # the HF conv1d shape
+
+
+def test_shards_keep_triples_together_and_skip_mtp(tmp_path):
+    """Every shard holds whole matrices (qweight, scale and mn of one name together); mtp.*
+    tensors are read only on request, as load_packed does (weights.py:238-254)."""
+    from safetensors import safe_open
+    q = _FakeLinear(64, 256).nibbles()
+    items = [(f"layers.{i}.mlp.down_proj.weight", tuple(t.clone() for t in q)) for i in range(5)] + [("mtp.fc.weight", torch.ones(4))]
+    info = ck.write_packed(str(tmp_path), items, shard_bytes=10000)
+    assert info["shards"] == 3 and info["packed_bytes"] == 5 * (64 * 128 + 2 * 64 * 2 * 2) + 16
+    for f in sorted(tmp_path.glob("model-*.safetensors")):
+        keys = set(safe_open(str(f), framework="pt").keys())
+        for k in keys:
+            base = k.rsplit(".", 1)[0]
+            if k.endswith(".qweight"):
+                assert {base + ".scale", base + ".mn"} <= keys
+    assert "mtp.fc.weight" not in ck.read_tensors(str(tmp_path))
+    assert "mtp.fc.weight" in ck.read_tensors(str(tmp_path), with_mtp=True)

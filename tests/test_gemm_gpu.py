@@ -284,3 +284,50 @@ def test_qlinear_gate_up_layout(dev):
     q2, s2, m2 = gu.nibbles()
     assert torch.equal(q2, qd) and torch.equal(s2, sd) and torch.equal(m2, md)
     check_close(gu(x), o.gemm_exact(o.make_x(8, 1024, seed=24), p, s, m), "gate_up layout")
+
+
+_C2 = {}
+
+
+def _config2_case(N, K):
+    """Config-2 weights (fp16 scale/min) on the device and their float64 dense form, cached per
+    shape so the M sweep builds each only once."""
+    from tokenrush_amd import gfx950
+    if (N, K) not in _C2:
+        _C2.clear()
+        p, s, m = o.make_weights(N, K, seed=300 + N % 89, dtype="fp16")
+        B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "fp16"))
+        _C2[(N, K)] = (B, sp, mp, o.weights_f64(p, s, m))
+    return _C2[(N, K)]
+
+
+@pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
+@pytest.mark.parametrize("M", [2, 4, 24, 32])
+def test_config2_shapes_m_sweep(dev, N, K, M):
+    """The bench's M sweep (config 2 at M = 2, 4) and config 4's M = 32 verify GEMM (with
+    M = 24 between the row-tile boundaries) on every config-2 shape against float64."""
+    from tokenrush_amd import gfx950
+    say(f"config2 sweep N={N} K={K} M={M}")
+    B, sp, mp, W = _config2_case(N, K)
+    x = o.make_x(M, K, seed=400 + M)
+    check_close(gfx950.mul(dev_x(x), B, sp, mp), x.astype(np.float64) @ W.T, f"{N}x{K} M={M}")
+
+
+@pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
+@pytest.mark.parametrize("M", [17, 32])
+def test_config2_partials_two_row_tiles(dev, N, K, M):
+    """Partial mode above 16 rows (config 4 runs the o and down projections this way at M = 32):
+    every slot written, the slot sum matches float64 to the GEMM bar, and equals mul()'s output
+    after the bf16 rounding up to summation order."""
+    from tokenrush_amd import gfx950
+    say(f"config2 partials N={N} K={K} M={M}")
+    B, sp, mp, W = _config2_case(N, K)
+    x = o.make_x(M, K, seed=500 + M)
+    xd = dev_x(x)
+    part = torch.full((gfx950.partial_slots(N, K, M), M, N), float("nan"), device="cuda:0")
+    part.copy_(gfx950.mul_partial(xd, B, sp, mp))
+    assert part.shape[0] == gfx950.partial_slots(N, K, M) and not torch.isnan(part).any()
+    ref = x.astype(np.float64) @ W.T
+    check_close(part.sum(0), ref, f"partials {N}x{K} M={M}")
+    y = gfx950.mul(xd, B, sp, mp).float()
+    assert (part.sum(0) - y).abs().max().item() <= np.abs(ref).max() * 2 ** -8

@@ -16,62 +16,99 @@ from tokenrush_amd.attn import NSPLIT
 pytestmark = pytest.mark.gpu
 
 
+def _bf(t):
+    return t.to(torch.bfloat16).float()
+
+
+def _ref_lin(L, v):
+    """v @ W^T with the exact weight q * s + m (what the GEMM folds), fp32."""
+    q, s, m = L.nibbles()
+    codes = torch.stack([q & 0xF, q >> 4], -1).view(q.shape[0], -1).float()
+    G = s.shape[1]
+    W = codes.view(q.shape[0], G, -1) * s.float()[..., None] + m.float()[..., None]
+    return v @ W.view(q.shape[0], -1).t()
+
+
+def _ref_norm(x, w, eps):
+    return _bf(x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + w.float()))
+
+
+def _ref_silu_mul(u):
+    F = u.shape[1] // 2
+    gg, v = u[:, :F], u[:, F:2 * F]
+    return _bf(gg / (1 + torch.exp(-gg)) * v)
+
+
+def _npf(t):
+    return t.float().cpu().numpy()
+
+
+class _RefState:
+    """numpy copies of the decode state the float reference reads and updates, per layer on
+    demand (the full-size state is too large to copy whole)."""
+
+    def __init__(self, model):
+        st = model.state
+        self.model, self.pos, self.slot = model, int(st.pos), int(st.slot)
+        self.cos, self.sin = _npf(st.cos), _npf(st.sin)
+        self.gdn, self.attn = {}, {}
+
+    def gdn_layer(self, k):
+        if k not in self.gdn:
+            st = self.model.state
+            self.gdn[k] = [_npf(st.ring[k]), _npf(st.rec[:, k])]
+        return self.gdn[k]
+
+    def attn_layer(self, a):
+        if a not in self.attn:
+            st = self.model.state
+            self.attn[a] = [st.k[a].view(torch.uint8).cpu().numpy(), st.v[a].view(torch.uint8).cpu().numpy(),
+                            _npf(st.k_scale[a]), _npf(st.v_scale[a])]
+        return self.attn[a]
+
+
+def _ref_mixer(model, li, L, n, rs):
+    """The layer's mixer on normed rows n (fp32 [M, hidden]) -> (u, y): the bf16 projection and the
+    mixer output, the GDN step or FP8 attention restated by the oracle."""
+    cfg = model.cfg
+    u = _bf(_ref_lin(L.proj, n))
+    if L.attention:
+        kc, vc, ks, vs = rs.attn_layer(model.attn_index[li])
+        q, kc[:], vc[:], ks[:], vs[:] = oat.attn_prep(_npf(u), _npf(L.q_norm_w), _npf(L.k_norm_w), rs.cos, rs.sin,
+                                                      rs.pos, kc, vc, ks, vs, cfg.n_heads, cfg.n_kv_heads,
+                                                      cfg.head_dim, cfg.rotary_dim, cfg.eps)
+        y = oat.attn_decode(q, _npf(u), kc, vc, ks, vs, rs.pos, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                            nsplit=NSPLIT)
+    else:
+        g = cfg.gdn
+        ring, rec = rs.gdn_layer(model.gdn_index[li])
+        y, ring[:], rec_k = og.gdn_step(_npf(u), _npf(n), _npf(L.in_ba), ring, _npf(L.conv_w), _npf(L.A),
+                                        _npf(L.dt_bias), rec, rs.slot, _npf(L.norm_w), rs.pos, g.gdn_k_heads,
+                                        g.gdn_v_heads, g.gdn_k_dim, g.gdn_v_dim, cfg.eps)
+        rec[:] = rec_k
+    return u, torch.from_numpy(np.ascontiguousarray(y)).to(n.device)
+
+
 def _ref_body(model, x0):
     """Float reference of VerifyModel.body: exact weights q * s + m, fp32 matmuls, the same bf16
     rounding points as the kernels (projection outputs, residual stream, norm outputs)."""
     cfg = model.cfg
-    bf = lambda t: t.to(torch.bfloat16).float()
-
-    def lin(L, v):
-        q, s, m = L.nibbles()                       # exact weight q * s + m (what the GEMM folds)
-        codes = torch.stack([q & 0xF, q >> 4], -1).view(q.shape[0], -1).float()
-        G = s.shape[1]
-        W = codes.view(q.shape[0], G, -1) * s.float()[..., None] + m.float()[..., None]
-        return v @ W.view(q.shape[0], -1).t()
-
-    def norm(x, w):
-        return bf(x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.eps) * (1.0 + w.float()))
-
-    def silu_mul(u):
-        F = u.shape[1] // 2
-        gg, v = u[:, :F], u[:, F:2 * F]
-        return bf(gg / (1 + torch.exp(-gg)) * v)
-
-    st = model.state
-    npf = lambda t: t.float().cpu().numpy()
-    pos, slot = int(st.pos), int(st.slot)
-    ring, rec = npf(st.ring), npf(st.rec)
-    kc, vc = st.k.view(torch.uint8).cpu().numpy(), st.v.view(torch.uint8).cpu().numpy()
-    ks, vs, cos, sin = npf(st.k_scale), npf(st.v_scale), npf(st.cos), npf(st.sin)
-    g = cfg.gdn
+    rs = _RefState(model)
     x = x0.float()
     h = None
     for li, L in enumerate(model.layers):
         if h is not None:
-            x = bf(x + bf(h))
-        n = norm(x, L.ln1)
-        u = bf(lin(L.proj, n))
-        if L.attention:
-            a = model.attn_index[li]
-            q, kc[a], vc[a], ks[a], vs[a] = oat.attn_prep(npf(u), npf(L.q_norm_w), npf(L.k_norm_w), cos, sin, pos,
-                                                          kc[a], vc[a], ks[a], vs[a], cfg.n_heads, cfg.n_kv_heads,
-                                                          cfg.head_dim, cfg.rotary_dim, cfg.eps)
-            y = oat.attn_decode(q, npf(u), kc[a], vc[a], ks[a], vs[a], pos, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
-                                nsplit=NSPLIT)
-        else:
-            k = model.gdn_index[li]
-            y, ring[k], rec_k = og.gdn_step(npf(u), npf(n), npf(L.in_ba), ring[k], npf(L.conv_w), npf(L.A),
-                                            npf(L.dt_bias), rec[:, k], slot, npf(L.norm_w), pos, g.gdn_k_heads,
-                                            g.gdn_v_heads, g.gdn_k_dim, g.gdn_v_dim, cfg.eps)
-            rec[:, k] = rec_k
-        h = lin(L.out, torch.from_numpy(y).to(x.device))
-        x = bf(x + bf(h))
-        n = norm(x, L.ln2)
-        a = silu_mul(bf(lin(L.gate_up, n)))
-        h = lin(L.down, a)
-    x = bf(x + bf(h))
-    n = norm(x, model.final_norm)
-    return lin(model.lm_head, n)
+            x = _bf(x + _bf(h))
+        n = _ref_norm(x, L.ln1, cfg.eps)
+        _, y = _ref_mixer(model, li, L, n, rs)
+        h = _ref_lin(L.out, y)
+        x = _bf(x + _bf(h))
+        n = _ref_norm(x, L.ln2, cfg.eps)
+        a = _ref_silu_mul(_bf(_ref_lin(L.gate_up, n)))
+        h = _ref_lin(L.down, a)
+    x = _bf(x + _bf(h))
+    n = _ref_norm(x, model.final_norm, cfg.eps)
+    return _ref_lin(model.lm_head, n)
 
 
 @pytest.fixture(scope="module")

@@ -727,15 +727,22 @@ __global__ __launch_bounds__(64) void residual_phase3_kernel(ResidualArgs a) {
 // Moves the accepted path's rows to consecutive positions: for every plane (layer x kv head),
 // row base + commit[t] -> row base + t for t = 1..n, where base = pos - n - 1 (pos already
 // advanced by the accept kernel). Rows are read into registers before any is written.
+// A commit that would touch rows outside the cache, or more than max_n rows, moves nothing and
+// sets *status (when given) to 1; status is left alone otherwise.
 __global__ void commit_rows_kernel(uint8_t* data, int planes, long plane_stride, int row_bytes, const int64_t* pos,
-                                   const int64_t* n_accepted, const int64_t* commit, int max_n) {
+                                   const int64_t* n_accepted, const int64_t* commit, int max_n, int* status) {
   const int plane = blockIdx.x;
   if (plane >= planes) return;
   const int n = (int)*n_accepted;
   const int64_t base = *pos - n - 1;
   const int64_t max_len = plane_stride / row_bytes;
-  for (int t = 1; t <= n && t <= max_n; ++t)  // rows outside the cache: commit nothing
-    if (base < 0 || base + commit[t] >= max_len || base + t >= max_len || commit[t] < 0) return;
+  bool bad = n > max_n || n < 0;
+  for (int t = 1; t <= n && t <= max_n; ++t)
+    bad |= base < 0 || base + commit[t] >= max_len || base + t >= max_len || commit[t] < 0;
+  if (bad) {
+    if (status && plane == 0 && threadIdx.x == 0) *status = 1;
+    return;
+  }
   uint8_t* p = data + (size_t)plane * plane_stride;
   // each thread moves 4-byte words; row_bytes % 4 == 0
   const int words = row_bytes / 4;
@@ -954,11 +961,11 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
 }
 
 int tr_commit_rows(void* data, int planes, long plane_stride_bytes, int row_bytes, const int64_t* pos,
-                   const int64_t* n_accepted, const int64_t* commit, int max_n, void* stream) {
+                   const int64_t* n_accepted, const int64_t* commit, int max_n, int* status, void* stream) {
   if (!data || !pos || !n_accepted || !commit) return TR_ERR_ARG;
   if (planes < 1 || row_bytes < 4 || row_bytes % 4 || max_n < 0 || max_n > 32) return TR_ERR_SHAPE;
   hipLaunchKernelGGL(commit_rows_kernel, dim3(planes), dim3(256), 0, (hipStream_t)stream, (uint8_t*)data, planes,
-                     plane_stride_bytes, row_bytes, pos, n_accepted, commit, max_n);
+                     plane_stride_bytes, row_bytes, pos, n_accepted, commit, max_n, status);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 

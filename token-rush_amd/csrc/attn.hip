@@ -104,7 +104,12 @@ struct AttnPrepArgs {
 // One wave per (head, token); lane l holds dims 4 l .. 4 l + 3.
 __global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
   const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-  const int64_t p = *a.pos + t;
+  // Positions past the cache's end: the rope table (maxlen rows) is read at the last row and no
+  // cache row is written (the split kernel reads at most maxlen rows), so nothing outside the
+  // cache is touched whatever the device position holds.
+  const int64_t p_raw = *a.pos + t;
+  const bool in_cache = p_raw >= 0 && p_raw < a.maxlen;
+  const int64_t p = in_cache ? p_raw : (p_raw < 0 ? 0 : a.maxlen - 1);
   const bool isq = head < a.HQ;
   const int j = head - a.HQ;
   const uint16_t* row = a.qkv + (size_t)t * a.ld;
@@ -160,6 +165,7 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
     *(uint2*)qo = st;
     return;
   }
+  if (!in_cache) return;
   // key: fp8 with one scale per (head, position)
   float am = fmaxf(fmaxf(fabsf(out[0]), fabsf(out[1])), fmaxf(fabsf(out[2]), fabsf(out[3])));
 #pragma unroll
@@ -238,7 +244,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
 
   // Cache reads go through buffer resources sized to the L live rows: rows past them, and the
   // prefetch past the split's last block, read zeros with no memory access and no branch.
-  const int liveL = (int)L;
+  const int liveL = (int)min(max(L, (int64_t)0), (int64_t)a.maxlen);   // never past the cache
   const auto krs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_cache + (size_t)j * a.maxlen * kAttnD), (short)0,
                                                      liveL * kAttnD, 0x00020000);
   const auto vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_cache + (size_t)j * a.maxlen * kAttnD), (short)0,

@@ -24,12 +24,12 @@
 //   channels for the M tokens (one thread per channel; the ring update), the L2 normalisation
 //   of q and k (a 256-channel workgroup holds two whole heads), and the gate dot products
 //   (one workgroup per gate row, the four waves splitting the hidden dim).
-//   gdn_step_kernel runs the recurrence, one workgroup of four waves per (value head, 32-column
-//   block): 48 x 4 = 192 workgroups, so the M x 64 KB-per-head snapshot stores -- the kernel's
-//   cost -- spread over most CUs. Wave w holds rows 32 w .. 32 w + 31 of the block's [128 x 32]
-//   state tile; lane (vq = l % 8, kg = l / 8) holds rows 32 w + 4 kg .. + 3, columns 4 vq .. + 3,
-//   in registers for all M tokens, and its snapshot stores are 16-byte vectors, 8 lanes per
-//   128-byte row segment. Sums over k: a lane's 4 rows, the wave's 8 row groups (DPP / permlane
+//   gdn_step_kernel runs the recurrence, one workgroup of four waves per (value head, 16-column
+//   block): 48 x 8 = 384 workgroups, so the M x 64 KB-per-head snapshot stores -- the kernel's
+//   cost -- spread over every CU. Wave w holds rows 32 w .. 32 w + 31 of the block's [128 x 16]
+//   state tile; lane (vq = l % 8, kg = l / 8) holds rows 32 w + 4 kg .. + 3, columns 2 vq, 2 vq + 1,
+//   in registers for all M tokens, and its snapshot stores are 8-byte vectors, 8 lanes per
+//   64-byte row segment. Sums over k: a lane's 4 rows, the wave's 8 row groups (DPP / permlane
 //   steps) and the 4 waves (LDS, fixed order), once per token for both o_t and kv_{t+1}.
 //   The gated norm needs the whole head: the four blocks store bf16 o with agent-scope stores,
 //   and the last of them to arrive normalizes the head for every token.

@@ -44,7 +44,7 @@ SIGNATURES = {
     "tr_sample": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _S, _P, _P]),
     "tr_accept_sample": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tr_accept_residual": (_I, [_P, _I, _I, _P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P]),
-    "tr_commit_rows": (_I, [_P, _I, ctypes.c_long, _I, _P, _P, _P, _I, _P]),
+    "tr_commit_rows": (_I, [_P, _I, ctypes.c_long, _I, _P, _P, _P, _I, _P, _P]),
     "tr_add_rmsnorm": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _I, ctypes.c_float, _I, _P]),
     "tr_silu_mul": (_I, [_P, ctypes.c_long, _P, _I, _I, _P]),
     "tr_gdn_workspace_bytes": (_S, [_I, _I, _I]),
@@ -90,3 +90,21 @@ def require_gpu(*ts):
     for t in ts:
         if t is not None and not t.is_cuda:
             raise RuntimeError("tokenrush_amd kernels take device tensors (no CPU path)")
+
+
+# Workspaces replaced by larger ones. They stay allocated until the process ends: a hipGraph
+# captured earlier still holds their addresses, and freeing them would let the caching
+# allocator hand that memory to other tensors which a later replay would then overwrite.
+_retired = []
+
+
+def grown_workspace(registry: dict, key, need: int, device, zero: bool = True) -> torch.Tensor:
+    """registry[key], replaced by a new uint8 buffer of at least `need` bytes (zero-filled when
+    `zero`) if it is missing or smaller; the buffer it replaces is kept alive."""
+    ws = registry.get(key)
+    if ws is None or ws.numel() < need:
+        if ws is not None:
+            _retired.append(ws)
+        ws = (torch.zeros if zero else torch.empty)(max(need, 256), dtype=torch.uint8, device=device)
+        registry[key] = ws
+    return ws

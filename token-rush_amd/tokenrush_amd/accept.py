@@ -104,25 +104,37 @@ def accept_tree(logits: torch.Tensor, node_toks: torch.Tensor, parent: torch.Ten
     return st
 
 
-def commit_rows(cache: torch.Tensor, st: AcceptState, max_n: int = 31):
-    """Tree commit: in every plane of `cache` [planes, max_len, row...] move the accepted path's
-    rows (written at pos_before + node) to consecutive positions pos_before + 1..n. For the
-    reference's fp8 KV cache [n_attn, kv_heads, max_len, head_dim] and its fp32 scales
-    [n_attn, kv_heads, max_len] (tokenrush/state.py:19-29) call it once per tensor."""
+def commit_rows(cache: torch.Tensor, st: AcceptState, layout: str, max_n: int = None,
+                status: torch.Tensor = None):
+    """Tree commit: in every plane of `cache` move the accepted path's rows (written at
+    pos_before + node) to consecutive positions pos_before + 1..n. layout names where the
+    position axis is: "rows" for [..., max_len, row] (the fp8 KV cache [n_attn, kv_heads,
+    max_len, head_dim]), "scalars" for [..., max_len] (its fp32 scales [n_attn, kv_heads,
+    max_len]; tokenrush/state.py:19-29). max_n defaults to the st.M - 1 drafts an accept can
+    keep. A commit that would reach rows outside the cache, or move more than max_n rows, moves
+    nothing and sets status (a device int32 [1], optional) to 1."""
     _lib.require_gpu(cache)
     if not cache.is_contiguous():
         raise RuntimeError("cache must be contiguous")
-    max_len = cache.shape[-2] if cache.dim() >= 4 else cache.shape[-1]
-    row_bytes = cache.element_size() * (cache.shape[-1] if cache.dim() >= 4 else 1)
-    lead = cache.dim() - (2 if cache.dim() >= 4 else 1)
-    planes = 1
-    for d in cache.shape[:lead]:
-        planes *= d
-    plane_stride = max_len * row_bytes
+    if layout == "rows":
+        if cache.dim() < 2:
+            raise RuntimeError("layout 'rows' needs [..., max_len, row]")
+        max_len, row_bytes, lead = cache.shape[-2], cache.shape[-1] * cache.element_size(), cache.shape[:-2]
+    elif layout == "scalars":
+        max_len, row_bytes, lead = cache.shape[-1], cache.element_size(), cache.shape[:-1]
+    else:
+        raise RuntimeError(f"layout must be 'rows' or 'scalars', got {layout!r}")
     if row_bytes % 4:
         raise RuntimeError("rows must be a multiple of 4 bytes")
-    rc = _lib.lib().tr_commit_rows(_lib.ptr(cache), planes, plane_stride, row_bytes, _lib.ptr(st.pos),
-                                   _lib.ptr(st.n_accepted), _lib.ptr(st.commit), max_n, _lib.stream_of(cache))
+    max_n = st.M - 1 if max_n is None else max_n
+    if status is not None and (status.dtype != torch.int32 or not status.is_cuda):
+        raise RuntimeError("status must be a device int32 tensor")
+    planes = 1
+    for d in lead:
+        planes *= d
+    rc = _lib.lib().tr_commit_rows(_lib.ptr(cache), planes, max_len * row_bytes, row_bytes, _lib.ptr(st.pos),
+                                   _lib.ptr(st.n_accepted), _lib.ptr(st.commit), max_n, _lib.ptr(status),
+                                   _lib.stream_of(cache))
     _lib.check(rc, "tr_commit_rows")
 
 
@@ -156,10 +168,7 @@ def lm_head_greedy(lm_head, hidden: torch.Tensor, spec_toks: torch.Tensor, st: A
             accept_greedy(logits, spec_toks, st)
         return logits if keep_logits else None
     key = hidden.device.index or 0
-    ws = _lm_ws.get(key)
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(need, dtype=torch.uint8, device=hidden.device)
-        _lm_ws[key] = ws
+    ws = _lib.grown_workspace(_lm_ws, key, need, hidden.device)
     logits = torch.empty(M, V, dtype=torch.bfloat16, device=hidden.device) if keep_logits else None
     spec = None if spec_toks is None else spec_toks[:M].to(torch.long).contiguous()
     x = hidden.contiguous()

@@ -84,11 +84,7 @@ def workspace(M: int, HQ: int, nsplit: int, device):
     if need == 0:
         raise RuntimeError(f"attention workspace: unsupported M={M}")
     key = torch.device(device).index or 0
-    ws = _ws.get(key)
-    if ws is None or ws.numel() < need:
-        ws = torch.empty(need, dtype=torch.uint8, device=device)
-        _ws[key] = ws
-    return ws
+    return _lib.grown_workspace(_ws, key, need, device, zero=False)
 
 
 def attn_decode_fused(q, qkv, k_cache, v_cache, pos_t, cfg, k_scale=None, v_scale=None, NSPLIT=NSPLIT):

@@ -73,8 +73,12 @@ def config_json(cfg) -> dict:
 
 # ------------------------------------------------------------------ tensors
 
-def read_tensors(path: str, device="cpu") -> dict:
-    """Every tensor of the packed checkpoint's shards, by name (weights.py:238-254; mtp.* kept)."""
+MTP_PREFIX = "mtp."   # the draft head's tensors: loaded only on request (weights.py:238-254)
+
+
+def read_tensors(path: str, device="cpu", with_mtp: bool = False) -> dict:
+    """Every tensor of the packed checkpoint's shards, by name (weights.py:238-254); the mtp.*
+    draft-head tensors are skipped unless with_mtp, as load_packed skips them."""
     shards = sorted(glob.glob(os.path.join(path, "model-*.safetensors")))
     if not shards:
         raise RuntimeError(f"{path}: no model-*.safetensors shards")
@@ -82,44 +86,50 @@ def read_tensors(path: str, device="cpu") -> dict:
     for shard in shards:
         with safe_open(shard, framework="pt", device=str(device)) as f:
             for name in f.keys():
-                out[name] = f.get_tensor(name)
+                if with_mtp or not name.startswith(MTP_PREFIX):
+                    out[name] = f.get_tensor(name)
     return out
 
 
+def _stored(name: str, v):
+    """The tensors one item is stored as, (key, CPU tensor): a plain tensor under its name, a
+    quantized matrix (qweight, scale, mn) as name.qweight, name.scale and name.mn."""
+    pairs = zip((name + ".qweight", name + ".scale", name + ".mn"), v) if isinstance(v, tuple) else [(name, v)]
+    return [(k, t.detach().cpu().contiguous()) for k, t in pairs]
+
+
+def _shard_plan(sizes, shard_bytes: int):
+    """Indices of `sizes` grouped into consecutive shards: a shard is closed at the first whole
+    matrix (all of its stored tensors) that brings it to shard_bytes or more."""
+    groups, cur, acc = [], [], 0
+    for i, n in enumerate(sizes):
+        cur.append(i)
+        acc += n
+        if acc >= shard_bytes:
+            groups.append(cur)
+            cur, acc = [], 0
+    return groups + ([cur] if cur else [])
+
+
 def write_packed(dst: str, items, cfg=None, group: int = GROUP, meta: dict = None, shard_bytes: int = 4 << 30):
-    """items: (name, tensor) or (name, (qweight, scale, mn)) -> shards + tokenrush.json (+ config.json
-    from cfg), the layout of weights.py:60-102."""
+    """Write the packed checkpoint format: the tensors in model-NNNNN.safetensors shards of about
+    shard_bytes each (a matrix's triple never straddles two shards), tokenrush.json with the
+    format, group, quantized names, shard count and stored bytes (weights.py:60-102), and
+    config.json from cfg when given."""
     os.makedirs(dst, exist_ok=True)
-    buf, size, shard, quantized, total = {}, 0, 0, [], 0
-
-    def flush():
-        nonlocal buf, size, shard
-        if buf:
-            save_file(buf, os.path.join(dst, f"model-{shard:05d}.safetensors"))
-            shard += 1
-            buf, size = {}, 0
-
-    for name, v in items:
-        if isinstance(v, tuple):
-            q, s, m = v
-            outs = {name + ".qweight": q, name + ".scale": s, name + ".mn": m}
-            quantized.append(name)
-        else:
-            outs = {name: v}
-        for k, t in outs.items():
-            t = t.detach().cpu().contiguous()
-            buf[k] = t
-            n = t.numel() * t.element_size()
-            size += n
-            total += n
-        if size >= shard_bytes:
-            flush()
-    flush()
-    info = {"format": "int4", "group": group, "quantized": quantized, "shards": shard, "packed_bytes": total}
+    units = [(_stored(name, v), isinstance(v, tuple), name) for name, v in items]
+    sizes = [sum(t.numel() * t.element_size() for _, t in ents) for ents, _, _ in units]
+    plan = _shard_plan(sizes, shard_bytes)
+    for si, idx in enumerate(plan):
+        save_file({k: t for i in idx for k, t in units[i][0]}, os.path.join(dst, f"model-{si:05d}.safetensors"))
+    info = dict(format="int4", group=group, quantized=[name for _, q, name in units if q], shards=len(plan),
+                packed_bytes=sum(sizes))
     info.update(meta or {})
-    json.dump(info, open(os.path.join(dst, PACK_META), "w"), indent=1)
+    with open(os.path.join(dst, PACK_META), "w") as f:
+        json.dump(info, f, indent=1)
     if cfg is not None:
-        json.dump(config_json(cfg), open(os.path.join(dst, "config.json"), "w"), indent=1)
+        with open(os.path.join(dst, "config.json"), "w") as f:
+            json.dump(config_json(cfg), f, indent=1)
     return info
 
 
@@ -162,3 +172,30 @@ def layer_items(L, li: int):
     out += [(p + "mlp.gate_proj.weight", (q[:F], s[:F], mn[:F])), (p + "mlp.up_proj.weight", (q[F:], s[F:], mn[F:])),
             (p + "mlp.down_proj.weight", L.down.nibbles())]
     return out
+
+
+def model_items(model):
+    """(name, tensor or triple) of a whole step.VerifyModel: its layers, the final norm, the
+    lm_head and the embedding table."""
+    items = [it for li, L in enumerate(model.layers) for it in layer_items(L, li)]
+    return items + [("norm.weight", model.final_norm), ("lm_head.weight", model.lm_head.nibbles()),
+                    ("embed_tokens.weight", model.embed)]
+
+
+def required_names(cfg) -> set:
+    """Every name the reference's loader reads for a model of this config (build_layer and
+    build_weights, weights.py:180-211): per layer its mixer's tensors, the MLP and the two norms,
+    then embed_tokens, norm and lm_head."""
+    names = {"embed_tokens.weight", "norm.weight", "lm_head.weight"}
+    for li in range(cfg.n_layers):
+        p = f"layers.{li}."
+        names |= {p + "input_layernorm.weight", p + "post_attention_layernorm.weight",
+                  p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight", p + "mlp.down_proj.weight"}
+        if cfg.is_attention(li):
+            names |= {p + "self_attn." + n for n in ("q_proj.weight", "k_proj.weight", "v_proj.weight",
+                                                     "o_proj.weight", "q_norm.weight", "k_norm.weight")}
+        else:
+            names |= {p + "linear_attn." + n for n in ("in_proj_qkv.weight", "in_proj_z.weight", "in_proj_b.weight",
+                                                       "in_proj_a.weight", "conv1d.weight", "A_log", "dt_bias",
+                                                       "norm.weight", "out_proj.weight")}
+    return names

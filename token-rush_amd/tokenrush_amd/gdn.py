@@ -48,11 +48,7 @@ def workspace(M: int, H: int, HV: int, device):
     if need == 0:
         raise RuntimeError(f"gdn workspace: unsupported M={M}, H={H} or HV={HV}")
     key = torch.device(device).index or 0
-    ws = _ws.get(key)
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(need, dtype=torch.uint8, device=device)
-        _ws[key] = ws
-    return ws
+    return _lib.grown_workspace(_ws, key, need, device)
 
 
 def gdn_step_fused(qkvz, x, ba_w, ring, conv_w, A, dt_bias, rec, slot, norm_w, pos_t, cfg, eps):

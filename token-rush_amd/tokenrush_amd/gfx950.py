@@ -118,13 +118,10 @@ def workspaces(N: int, device, K: int = None, M: int = MAX_ROWS, min_bytes: int 
     construction). Zero-filled: its counters must read zero between calls, which every call
     restores. Calls that overlap on one device (different streams) would share it."""
     key = torch.device(device).index or 0
-    ws = _ws.get(key)
     need = min_bytes
     if K is not None:
         need = max([need] + [workspace_bytes(N, K, mm) for mm in {1, min(M, 16), M}])
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
-        _ws[key] = ws
+    ws = _lib.grown_workspace(_ws, key, need, device)
     return ws, ws.numel()
 
 

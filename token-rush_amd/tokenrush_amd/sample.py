@@ -41,11 +41,7 @@ def workspace(M: int, V: int, device):
     need = int(_lib.lib().tr_accept_workspace_bytes(M, V))
     if need == 0:
         raise RuntimeError(f"accept shape (M={M}, V={V}) not supported: need 1 <= M <= 32, 64 <= V <= 262144")
-    ws = _ws.get(key)
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(need, dtype=torch.uint8, device=device)
-        _ws[key] = ws
-    return ws
+    return _lib.grown_workspace(_ws, key, need, device)
 
 
 def _check_logits(logits):

@@ -26,8 +26,9 @@ kernels of this package:
 The decode state (tokenrush/state.py:14-43) lives on the device: the position and the committed
 recurrent-state slot (read by the mixers, written by the accept), the conv rings and the fp32
 recurrent state in 8 snapshot slots per GDN layer, and the FP8 KV cache with per-(head, position)
-scales per attention layer, preloaded with `live` random tokens. The embedding gather is replaced
-by the step's input buffer x0.
+scales per attention layer, preloaded with `live` random tokens. The step reads its input rows from
+the buffer x0 (what the embedding gather of the verify tokens produces); the embedding table itself
+is kept for checkpoints.
 """
 from dataclasses import dataclass
 
@@ -239,11 +240,15 @@ class VerifyModel:
             self.layers = [Layer(cfg, li, gen, self.device) for li in range(cfg.n_layers)]
             self.final_norm = _bf16((cfg.hidden,), 0.1, gen, self.device)
             self.lm_head = _random_linear(cfg.vocab, cfg.hidden, gen, self.device)
+            # the step takes its input rows x0 directly; the table is kept so that a saved
+            # checkpoint holds every tensor the reference's loader reads
+            self.embed = _bf16((cfg.vocab, cfg.hidden), 0.02, gen, self.device)
         else:
             from .checkpoint import linear
             self.layers = [Layer.from_tensors(cfg, li, tensors, self.device) for li in range(cfg.n_layers)]
             self.final_norm = tensors["norm.weight"].to(self.device)
             self.lm_head = linear(tensors, "lm_head.weight", self.device)
+            self.embed = tensors["embed_tokens.weight"].to(self.device)
         self.gdn_index, self.attn_index = {}, {}
         for li, L in enumerate(self.layers):
             d = self.attn_index if L.attention else self.gdn_index
@@ -290,15 +295,14 @@ class VerifyModel:
         return cls(read_config(path, **cfg_overrides), device=device, seed=seed, tensors=read_tensors(path))
 
     def save_checkpoint(self, dst: str, meta: dict = None):
-        """Write the weights in the packed checkpoint format (weights.py:60-102)."""
-        from .checkpoint import layer_items, write_packed
-
-        def items():
-            for li, L in enumerate(self.layers):
-                yield from layer_items(L, li)
-            yield "norm.weight", self.final_norm
-            yield "lm_head.weight", self.lm_head.nibbles()
-        return write_packed(dst, items(), self.cfg, meta=meta)
+        """Write the weights in the packed checkpoint format (weights.py:60-102): every tensor the
+        reference's build_weights reads (weights.py:185-211), checked before anything is written."""
+        from .checkpoint import model_items, required_names, write_packed
+        items = model_items(self)
+        missing = required_names(self.cfg) - {n for n, _ in items}
+        if missing:
+            raise RuntimeError(f"checkpoint would miss {sorted(missing)[:4]}")
+        return write_packed(dst, items, self.cfg, meta=meta)
 
     def body(self, x0: torch.Tensor) -> torch.Tensor:
         """x0 [M, hidden] bf16 -> logits [M, vocab] bf16, at the state's position and slot."""
