@@ -6,7 +6,7 @@
  * error code. That makes every call recordable by hipGraph stream capture.
  *
  * Error codes: 0 ok; 1 problem shape not supported; 2 no kernel configuration; 3 bad argument;
- * 4 launch failed. 1 and 2 mean what the reference's Marlin launcher means by them
+ * 4 launch failed; 5 the call needs more than a no-allocation entry point's fixed scratch. 1 and 2 mean what the reference's Marlin launcher means by them
  * (tokenrush/csrc/marlin_bf16.cu:627-669, surfaced by marlin_bf16.cpp:41-43).
  *
  * Tensor conventions (row-major, contiguous):
@@ -54,6 +54,18 @@ int tr_int4_gemm(const void* x, const void* packed, void* out, void* partials, v
 int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials, void* workspace,
                     size_t workspace_bytes, int M, int N, int K, int group, int scale_dtype, int n_slots,
                     int R, void* stream);
+
+/* tr_int4_gemm in out mode (bf16 [M, N]) with no workspace argument and no allocation: the
+ * K-slot partials and arrival counters live in a fixed 16 MiB device array of the library (one
+ * copy per GPU, held until the process ends), found with hipGetSymbolAddress on the first call
+ * on each device (which also clears its counters with a fill kernel on `stream`). Calls whose
+ * workspace need (tr_gemm_workspace_bytes(N, K, M)) exceeds 16 MiB return 5 (TR_ERR_SCRATCH).
+ * Every call on one GPU shares that array and leaves its counters at zero; calls that overlap on
+ * one GPU (different streams) race. Same results, bit for bit, as tr_int4_gemm.
+ * No counterpart in the reference: for callers that cannot allocate (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). */
+int tr_int4_gemm_noalloc(const void* x, const void* packed, void* out, int M, int N, int K, int group, int scale_dtype,
+                         void* stream);
 
 /* Fused gate/up + activation: packed is a [gate (N/2 rows); up (N/2 rows)] weight packed by
  * tr_pack_int4_pairs; out bf16 [M, N/2] = silu(bf16(x . gate^T)) * bf16(x . up^T), bit for bit what

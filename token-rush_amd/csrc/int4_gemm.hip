@@ -43,6 +43,8 @@
 // tokenrush/marlin.py:158-168) or a workspace the last-arriving slot reduces into bf16.
 #include "accept_common.h"
 
+#include <mutex>
+
 namespace tr {
 
 constexpr int kGroup = 128;
@@ -822,6 +824,68 @@ static int gemm_impl(const void* x, const void* packed, void* out, void* partial
     a.ws_part = (float*)((char*)workspace + ws_counter_bytes());
   }
   return launch(a, p, scale_dtype, (hipStream_t)stream) == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+}  // extern "C"
+
+// ----------------------------------------------------------------------------- no-allocation variant
+//
+// tr_int4_gemm_noalloc takes its workspace from `scratch`, a fixed device array of this library,
+// instead of a caller's buffer: the counter region (zero between calls) then the fp32 partials of
+// the K slots. Every GPU that runs the library holds its own copy until the process ends. In host
+// code `scratch` names a host-side stand-in, never the device memory: the device address comes
+// from hipGetSymbolAddress, once per device, and only that address reaches a kernel.
+namespace {
+
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static_assert(kScratchBytes > (size_t)4096 * 32 * sizeof(int), "scratch holds the counter region and partials");
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];  // the device address of `scratch` on each device, once looked up
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// The current device's scratch address. The first call on a device looks it up and clears the
+// counter region with a fill kernel on `stream` (a kernel, not a memset, so that a first call
+// under graph capture records a node that is valid on every replay).
+int device_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TR_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TR_ERR_LAUNCH;
+    const int words = (int)(ws_counter_bytes() / sizeof(uint32_t));
+    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, stream, (uint32_t*)p, words);
+    if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return TR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tr_int4_gemm_noalloc(const void* x, const void* packed, void* out, int M, int N, int K, int group, int scale_dtype,
+                         void* stream) {
+  if (group != kGroup) return TR_ERR_CONFIG;
+  if (M < 0 || M > 32 || !shape_ok(N, K)) return TR_ERR_SHAPE;
+  if (M == 0) return TR_OK;
+  const size_t need = tr_gemm_workspace_bytes(N, K, M);
+  if (need > kScratchBytes) return TR_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = device_scratch((hipStream_t)stream, &ws);
+    if (rc != TR_OK) return rc;
+  }
+  return gemm_impl(x, packed, out, nullptr, ws, need > 0 ? kScratchBytes : 0, M, N, K, group, scale_dtype, 0, 0, 0,
+                   stream);
 }
 
 int tr_int4_gemm_ex(const void* x, const void* packed, void* out, void* partials, void* workspace,

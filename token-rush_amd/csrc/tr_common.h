@@ -16,6 +16,7 @@ enum {
   TR_ERR_CONFIG = 2,     // no kernel configuration for the requested tiling
   TR_ERR_ARG = 3,        // null pointer / bad enum / bad size
   TR_ERR_LAUNCH = 4,     // the HIP launch itself failed
+  TR_ERR_SCRATCH = 5,    // the call needs more than the fixed device scratch of a no-allocation entry point
 };
 
 // bf16 bits -> fp32 (exact).

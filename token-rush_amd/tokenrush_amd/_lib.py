@@ -15,9 +15,10 @@ LIB_PATH = os.path.join(_HERE, "libtrhip.so")
 
 # Error codes (tr_common.h). 1 and 2 mean what the reference's Marlin launcher means by
 # them (marlin_bf16.cu:627-669, marlin_bf16.cpp:41-43).
-OK, ERR_SHAPE, ERR_CONFIG, ERR_ARG, ERR_LAUNCH = 0, 1, 2, 3, 4
+OK, ERR_SHAPE, ERR_CONFIG, ERR_ARG, ERR_LAUNCH, ERR_SCRATCH = 0, 1, 2, 3, 4, 5
 _ERRORS = {ERR_SHAPE: "problem shape not supported", ERR_CONFIG: "no kernel configuration",
-           ERR_ARG: "bad argument", ERR_LAUNCH: "kernel launch failed"}
+           ERR_ARG: "bad argument", ERR_LAUNCH: "kernel launch failed",
+           ERR_SCRATCH: "needs more than the 16 MiB device scratch of the no-allocation entry point"}
 
 _P, _I = ctypes.c_void_p, ctypes.c_int
 # name -> (restype, argtypes); the signatures of include/tokenrush_hip.h
@@ -29,6 +30,7 @@ SIGNATURES = {
     "tr_packed_bytes": (_S, [_I, _I]),
     "tr_int4_gemm": (_I, [_P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _I, _P]),
     "tr_int4_gemm_ex": (_I, [_P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "tr_int4_gemm_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "tr_int4_gemm_silu": (_I, [_P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P]),
     "tr_pack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "tr_unpack_int4": (_I, [_P, _P, _P, _P, _I, _I, _P]),
