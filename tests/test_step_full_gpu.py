@@ -130,3 +130,110 @@ def test_full_size_step_accept_and_graph_replay(full_model):
         _ = m.body(x0)                                  # eager work between replays
         torch.cuda.synchronize()
     del graph
+
+
+def _capture_and_replay(m, reset, run, st, eager, x0, reps=3):
+    """Capture run() as one graph, replay it from the restored state `reps` times (eager work in
+    between) and compare logits and accept outputs with the eager step bit for bit."""
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        reset()
+        run()                                           # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        lg_g = run()
+    for rep in range(reps):
+        reset()
+        st.n_accepted.fill_(-1)
+        st.tokens.fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (lg_g, st.n_accepted, st.tok, st.pos, st.slot, st.tokens, st.commit)
+        for name, a, b in zip(("logits", "n", "tok", "pos", "slot", "tokens", "commit"), got, eager):
+            assert torch.equal(a, b), (rep, name)
+        _ = m.body(x0)                                  # eager work between replays
+        torch.cuda.synchronize()
+    del graph
+
+
+def _check_accept(st, want):
+    pad = [-1] * (M - want["n"] - 1)
+    assert int(st.n_accepted) == want["n"] and int(st.tok) == want["tok"] and int(st.pos) == want["pos"]
+    assert int(st.slot) == want["n"] and st.tokens.cpu().tolist() == want["tokens"] + pad
+    assert st.commit.cpu().tolist() == want["commit"] + pad
+
+
+def test_full_size_sampled_step_in_one_graph(full_model):
+    """The reference's sampled verify (model.py:306: pred = sample(logits, params, u)) inside the
+    step graph: device SamplingParams, uniforms supplied; drafts planted from an eager pass so 3
+    are accepted; the accept against oracle.sample + verify_chain on the step's own logits."""
+    from tokenrush_amd.accept import AcceptState
+    from tokenrush_amd.sample import SamplingParams
+    m = full_model
+    print("config-5 sampled step", flush=True)
+    g = torch.Generator(device="cuda:0").manual_seed(12)
+    x0 = torch.randn(M, m.cfg.hidden, device="cuda:0", generator=g).to(torch.bfloat16)
+    st, live, V = AcceptState(M, "cuda:0"), m.cfg.live, m.cfg.vocab
+    params = SamplingParams("cuda:0")
+    params.set(temperature=0.8, top_p=0.95, top_k=40)
+    u = torch.rand(M, device="cuda:0", generator=g)
+
+    def reset():
+        m.state.restore(m.initial_state)
+        st.pos.fill_(live)
+        st.slot.zero_()
+
+    def logits_np(lg):
+        return oa.logits_f32(lg.view(torch.int16).cpu().numpy().view(np.uint16))
+
+    reset()
+    lg0 = logits_np(m.body(x0))
+    pred = oa.sample(lg0, 0.8, 0.95, 40, u.cpu().numpy())
+    spec = np.zeros(M, dtype=np.int64)
+    spec[0] = 3
+    spec[1:4] = pred[0:3]
+    spec[4:] = (pred[3:7] + 1) % V
+    spec_t = torch.from_numpy(spec).to("cuda:0")
+    reset()
+    lg = m.step(x0, spec_t, st, params=params, u=u)
+    torch.cuda.synchronize()
+    want = oa.verify_chain(oa.sample(logits_np(lg), 0.8, 0.95, 40, u.cpu().numpy()), spec, pos=live)
+    assert want["n"] == 3
+    _check_accept(st, want)
+    eager = [t.clone() for t in (lg, st.n_accepted, st.tok, st.pos, st.slot, st.tokens, st.commit)]
+    _capture_and_replay(m, reset, lambda: m.step(x0, spec_t, st, params=params, u=u), st, eager, x0)
+
+
+def test_full_size_residual_step_in_one_graph(full_model):
+    """Residual rejection sampling after the full step (draft probabilities q [7, V], uniforms
+    supplied): the accept against oracle.residual_accept on the step's own logits; the step with
+    it captured as one graph reproduces the eager step bit for bit."""
+    from tokenrush_amd.accept import AcceptState
+    m = full_model
+    print("config-5 residual step", flush=True)
+    g = torch.Generator(device="cuda:0").manual_seed(13)
+    x0 = torch.randn(M, m.cfg.hidden, device="cuda:0", generator=g).to(torch.bfloat16)
+    st, live, V = AcceptState(M, "cuda:0"), m.cfg.live, m.cfg.vocab
+    reset_state = lambda: (m.state.restore(m.initial_state), st.pos.fill_(live), st.slot.zero_())
+    reset_state()
+    lg0 = m.body(x0).float()
+    # drafts 1..3 are the target's argmax with q = the target's own distribution (accepted for
+    # any u < 1); the rest are random tokens under a random draft distribution
+    q = torch.softmax(torch.randn(M - 1, V, device="cuda:0", generator=g) * 2, -1)
+    q[:3] = torch.softmax(lg0[:3], -1)
+    q = q.contiguous()
+    spec = torch.randint(0, V, (M,), device="cuda:0", generator=g)
+    spec[1:4] = lg0[:3].argmax(-1)
+    u = torch.rand(M, device="cuda:0", generator=g) * 0.9
+    reset_state()
+    lg = m.step(x0, spec, st, q=q, u=u)
+    torch.cuda.synchronize()
+    lg_np = oa.logits_f32(lg.view(torch.int16).cpu().numpy().view(np.uint16))
+    want = oa.residual_accept(lg_np, q.cpu().numpy(), spec[1:].cpu().numpy(), u.cpu().numpy(), pos=live)
+    assert want["n"] >= 3
+    _check_accept(st, want)
+    eager = [t.clone() for t in (lg, st.n_accepted, st.tok, st.pos, st.slot, st.tokens, st.commit)]
+    _capture_and_replay(m, reset_state, lambda: m.step(x0, spec, st, q=q, u=u), st, eager, x0)

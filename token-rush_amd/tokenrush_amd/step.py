@@ -35,7 +35,7 @@ from dataclasses import dataclass
 import torch
 
 from . import gfx950
-from .accept import AcceptState, lm_head_greedy
+from .accept import AcceptState, accept_residual, accept_sampled, lm_head_greedy
 from .attn import AttnConfig, attn_decode_fused, attn_prep, rope_table
 from .attn import NSPLIT as ATTN_NSPLIT
 from .attn import workspace as attn_workspace
@@ -43,6 +43,8 @@ from .fused import add_rmsnorm
 from .gdn import RING, GDNConfig, gdn_step_fused
 from .gdn import workspace as gdn_workspace
 from .quant import QLinear
+from .sample import SamplingParams
+from .sample import workspace as accept_workspace
 
 MAX_M = 8          # verify rows per step (1 committed + 7 drafts); also the snapshot slots
 
@@ -308,11 +310,28 @@ class VerifyModel:
         """x0 [M, hidden] bf16 -> logits [M, vocab] bf16, at the state's position and slot."""
         return self.lm_head(self.hidden(x0))
 
-    def step(self, x0: torch.Tensor, spec_toks: torch.Tensor, st: AcceptState) -> torch.Tensor:
-        """Body at st.pos / st.slot + lm_head with the greedy accept/commit in its epilogue (one
-        launch), which advances st.pos by n + 1 and sets st.slot = n. Returns the logits, kept as
-        the reference keeps them (model.py:300; graph-owned under capture)."""
-        return lm_head_greedy(self.lm_head, self.hidden(x0, st.pos, st.slot), spec_toks, st, keep_logits=True)
+    def step(self, x0: torch.Tensor, spec_toks: torch.Tensor, st: AcceptState, params: SamplingParams = None,
+             u: torch.Tensor = None, q: torch.Tensor = None) -> torch.Tensor:
+        """Body at st.pos / st.slot, the lm_head and the accept/commit, which advances st.pos by
+        n + 1 and sets st.slot = n (model.py:293-312). Returns the logits [M, vocab], kept as the
+        reference keeps them (model.py:300; graph-owned under capture). The accept rule:
+          greedy    (params None, q None): in the lm_head GEMM's epilogue, one launch;
+          sampled   (params given): pred = sample(logits, params, u) with the device-side
+                    SamplingParams and uniforms u [M] (drawn on the device when None, as
+                    sample.py:47-48 does), then the leading-match commit (model.py:306-312);
+          residual  (q given, fp32 [M - 1, vocab] draft probabilities, u [M]): rejection
+                    sampling with the residual resample."""
+        n = self.hidden(x0, st.pos, st.slot)
+        if params is None and q is None:
+            return lm_head_greedy(self.lm_head, n, spec_toks, st, keep_logits=True)
+        logits = self.lm_head(n)
+        if q is not None:
+            if u is None:
+                u = torch.rand(logits.shape[0], device=logits.device)
+            accept_residual(logits, q, spec_toks, u, st)
+        else:
+            accept_sampled(logits, spec_toks, params, st, u)
+        return logits
 
 
 def prepare(model: VerifyModel, M: int):
@@ -323,4 +342,5 @@ def prepare(model: VerifyModel, M: int):
             gfx950.workspaces(lin.shape[0], model.device, lin.shape[1], M)
     gfx950.workspaces(cfg.vocab, model.device, cfg.hidden, M)
     gdn_workspace(M, cfg.gdn_k_heads, cfg.gdn_v_heads, model.device)
+    accept_workspace(M, cfg.vocab, model.device)
     attn_workspace(M, cfg.n_heads, ATTN_NSPLIT, model.device)
