@@ -166,12 +166,13 @@ struct StripWalk {
   int m, s;         // current element's row and strip index
   int dm, ds;       // step T / P as rows and strips
   int M;
-  __device__ __forceinline__ StripWalk(int t, int lgP, int T, int M_) : M(M_) {
+  // magicM = ceil(2^32 / M) (M > 1): q / M = umulhi(q, magicM) exactly for the q < 2^16 used here
+  __device__ __forceinline__ StripWalk(int t, int lgP, int T, int M_, uint32_t magicM) : M(M_) {
     const int q = t >> lgP, dq = T >> lgP;
-    m = q % M_;
-    s = q / M_;
-    dm = dq % M_;
-    ds = dq / M_;
+    s = M_ == 1 ? q : (int)__umulhi((uint32_t)q, magicM);
+    m = q - s * M_;
+    ds = M_ == 1 ? dq : (int)__umulhi((uint32_t)dq, magicM);
+    dm = dq - ds * M_;
   }
   __device__ __forceinline__ void next() {
     m += dm;
@@ -190,6 +191,12 @@ struct GemmArgs {
   float* ws_part;         // fp32 [S, M, N] workspace (OUT_BF16_VIA_WS)
   int* ws_cnt;            // one counter per workgroup row range (<= N/16), zero between calls
   int M, N, K, S, R;      // R = strips per workgroup
+  // Launch constants computed on the host, so that the kernel's prologue (run by every wave,
+  // on the CU's shared scalar unit) needs no division: row workgroups gn = grid / S, workgroups
+  // rbi < rfull take R strips and the rest R - 1, K blocks nb = Gp / GW, the quad-row stride and
+  // the weight's size in bytes, and ceil(2^32 / S), ceil(2^32 / M) for exact small quotients.
+  int gn, rfull, nb, quad_stride, wbytes;
+  uint32_t magicS, magicM;
   int RB;                 // strips per LDS reduction batch
   int mode;
   int silu;               // 1: gate/up pair layout, out = silu(gate) * up, bf16 [M, N / 2]
@@ -203,6 +210,11 @@ struct GemmArgs {
   int xstage_off;         // byte offset of the activation staging area in dynamic LDS (M <= 8)
 };
 
+// q / d for q < 2^16 and 1 <= d < 2^15, magic = ceil(2^32 / d) (d == 1 has no 32-bit magic).
+__device__ __forceinline__ int udiv_small(uint32_t q, int d, uint32_t magic) {
+  return d == 1 ? (int)q : (int)__umulhi(q, magic);
+}
+
 // One accumulator tile element: (mt, lane, r) -> output row m = 16 mt + 4 (lane / 16) + r,
 // column n = 16 strip + lane % 16.
 template <int MT, int GW, bool F16S, bool XDMA>
@@ -211,23 +223,22 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   __shared__ uint64_t rowbest[32];  // fused argmax: best key per output row
   if (threadIdx.x < 32) rowbest[threadIdx.x] = 0;
   const int G = a.K / kGroup;
-  const int Gp = padded_groups(a.K);
-  const int nstrips = a.N / 16;
   const int W = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
-  const int slot = blockIdx.x % a.S;
-  const int rbi = blockIdx.x / a.S;
+  const int rbi = udiv_small(blockIdx.x, a.S, a.magicS);
+  const int slot = blockIdx.x - rbi * a.S;
   // Workgroup rbi of the grid_n row workgroups takes strips rbi, rbi + grid_n, ...: at any
   // moment all workgroups stream one contiguous band of the weight, which keeps their progress
   // even (contiguous per-workgroup ranges finish up to 3 us apart on the large shapes).
-  const int gn = gridDim.x / a.S;
+  const int gn = a.gn;
   const int r0 = 0;
-  const int r1 = (nstrips - rbi + gn - 1) / gn;
+  const int r1 = rbi < a.rfull ? a.R : a.R - 1;
   auto phys = [&](int r) { return rbi + r * gn; };
 
-  const int nb = Gp / GW;                              // K blocks (GW divides a quad)
-  const int b0 = (int)(((long)slot * nb) / a.S), b1 = (int)(((long)(slot + 1) * nb) / a.S);
+  const int nb = a.nb;                                 // K blocks (GW divides a quad)
+  const int b0 = udiv_small(slot * nb, a.S, a.magicS);
+  const int b1 = udiv_small((slot + 1) * nb, a.S, a.magicS);
   const int nw = b1 - b0;                              // active waves of this slot
   const bool active = wave < nw;
   const int gbase = (b0 + min(wave, nw - 1)) * GW;     // first group of this wave's block
@@ -237,9 +248,9 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // Byte offset of this wave's groups in strip r. Strips past the range get an offset beyond
   // the buffer resource's size: the hardware returns zeros for those loads without touching
   // memory, so every loop path issues the same loads (no vmcnt drain) and none re-reads HBM.
-  const int quad_stride = Gp / kQuad * kQuadBytes;
+  const int quad_stride = a.quad_stride;
   const int blk_off = gbase / kQuad * kQuadBytes + gbase % kQuad * kCodeBytes;
-  const int oob = nstrips * quad_stride;
+  const int oob = a.wbytes;
   auto strip_off = [&](int r) { return __builtin_amdgcn_readfirstlane(r < r1 ? phys(r) * quad_stride + blk_off : oob); };
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.packed, (short)0, oob, 0x00020000);
   const int lane_off = 16 * lane;
@@ -251,28 +262,26 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // Padding groups (g >= G) read group G - 1: finite values that meet zero scale and min.
   uint4 xa[GW][MT][4];
   if constexpr (XDMA) {
-    // M <= 8: load the rows coalesced -- a 64-lane load covers four whole 256-byte row segments
-    // of a group -- straight into this wave's LDS staging area (buffer_load ... lds, no VGPRs),
-    // then read them back in the operand layout. In the operand layout itself consecutive lanes
-    // would read different rows, each lane a separate cache access, which took 3-6 us for these
-    // 8 KB per wave. Chunk k of row r sits in 16-byte slot k ^ r of the row, so the 16 rows read
-    // by one operand load fall in different LDS banks. Rows >= M read zeros (out-of-range
-    // offsets: no memory access) and are never used.
-    static_assert(MT == 1, "activation staging covers one row tile");
+    // M <= 8: load the rows coalesced straight into this wave's LDS staging area
+    // (buffer_load ... lds, no VGPRs), then read them back in the operand layout. In the operand
+    // layout itself consecutive lanes would read different rows, each lane a separate cache
+    // access, which took 3-6 us for these 8 KB per wave. Load t brings row t of the wave's four
+    // groups (lane l: group l / 16, 16-byte chunk (l % 16) ^ t), so a call issues M loads, one per
+    // real row: every load instruction costs the CU's address unit the same 16 cycles whether
+    // its lanes fetch or not. The staging area holds row r of group gw at (r GW + gw) 256 bytes,
+    // chunk k of the row in 16-byte slot k ^ r, so the 16 rows read by one operand load fall in
+    // different LDS banks.
+    static_assert(MT == 1 && GW == 4, "activation staging covers one row tile and four groups");
     char* stage = (char*)red + a.xstage_off + wave * (GW * 2048);
-    const int xbytes = a.M * a.K * 2;
-    const auto xrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, xbytes, 0x00020000);
-    const int lr = lane >> 4, lk = lane & 15;
+    const auto xrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.M * a.K * 2, 0x00020000);
+    const int lk = lane & 15;
+    const int g = min(gbase + (lane >> 4), G - 1);
 #pragma unroll
-    for (int gw = 0; gw < GW; ++gw) {
-      const int g = min(gbase + gw, G - 1);
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int r = 4 * c + lr;
-        const int off = r < a.M ? (r * a.K + g * kGroup) * 2 + ((lk ^ r) & 15) * 16 : xbytes;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(stage + gw * 2048 + c * 1024),
-                                                 16, off, 0, 0, 0);
-      }
+    for (int t = 0; t < 8; ++t) {
+      if (t >= a.M) break;
+      const int off = (t * a.K + g * kGroup) * 2 + ((lk ^ t) & 15) * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(stage + t * 1024), 16, off,
+                                               0, 0, 0);
     }
   } else {
 #pragma unroll
@@ -291,6 +300,10 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // so waiting for the activations leaves the strips in flight). Waves without a K block issue
   // out-of-range loads: no memory access, the same count.
   Strip<GW> buf[2];
+  // Staged kernels: every wave's activation requests enter the CU's in-order memory pipeline
+  // before any wave's weight requests, so no wave waits for its activations behind the other
+  // waves' strips.
+  if constexpr (XDMA) __builtin_amdgcn_s_barrier();
   load_strip<GW>(buf[0], rsrc, active ? strip_off(r0) : oob, lane_off, sm_voff);
   load_strip<GW>(buf[1], rsrc, active ? strip_off(r0 + 1) : oob, lane_off, sm_voff);
   if constexpr (XDMA) {
@@ -302,7 +315,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int k = 4 * j + (lane >> 4);
-        const uint4 v = *(const uint4*)(stage + gw * 2048 + (i & 7) * 256 + ((k ^ i) & 15) * 16);
+        const uint4 v = *(const uint4*)(stage + ((i & 7) * GW + gw) * 256 + ((k ^ i) & 15) * 16);
         xa[gw][0][j] = i < a.M ? v : make_uint4(0u, 0u, 0u, 0u);
       }
     }
@@ -316,20 +329,26 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     const int sel = (lane & 15) >> 2;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      f32x4 D = {0.f, 0.f, 0.f, 0.f};
+      // one accumulator per group slot (independent MFMA chains); a lane's element of D is
+      // nonzero in exactly one of them, so their sum is exact
+      f32x4 D[GW];
 #pragma unroll
       for (int gw = 0; gw < GW; ++gw) {
         const uint32_t one = sel == gw ? 0x3F803F80u : 0u;
         const bf16x8 A = __builtin_bit_cast(bf16x8, make_uint4(one, one, one, one));
+        D[gw] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, xa[gw][mt][j]), D, 0, 0, 0);
+          D[gw] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, xa[gw][mt][j]), D[gw], 0, 0, 0);
       }
-      Xa[mt] = D[0];
+      float xs = D[0][0];
+#pragma unroll
+      for (int gw = 1; gw < GW; ++gw) xs += D[gw][0];
+      Xa[mt] = xs;
     }
   }
   const int slot16 = lane >> 4;
-  const StripWalk walk16(threadIdx.x, 4, blockDim.x, a.M), walk8(threadIdx.x, 3, blockDim.x, a.M);
+  const StripWalk walk16(threadIdx.x, 4, blockDim.x, a.M, a.magicM), walk8(threadIdx.x, 3, blockDim.x, a.M, a.magicM);
 
   // Partial tiles of RB consecutive strips are collected in LDS and reduced together (one
   // barrier per batch); batches alternate between two halves of the LDS ring, so the next
@@ -660,6 +679,9 @@ struct Plan {
   int GW, S, W, R, grid_n;
 };
 
+// ceil(2^32 / d) for 2 <= d < 2^15 (udiv_small's magic; d == 1 is handled there without one).
+uint32_t magic_div(int d) { return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + d - 1) / d); }
+
 int group_block(int M) { return M > 16 ? 2 : 4; }
 
 // Tiling of an N x K weight for M rows. Depends on M only through the row-tile count
@@ -786,6 +808,13 @@ static int gemm_impl(const void* x, const void* packed, void* out, void* partial
   a.K = K;
   a.S = p.S;
   a.R = p.R;
+  a.gn = p.grid_n;
+  a.rfull = N / 16 - (p.R - 1) * p.grid_n;
+  a.nb = padded_groups(K) / p.GW;
+  a.quad_stride = padded_groups(K) / kQuad * kQuadBytes;
+  a.wbytes = (int)packed_bytes(N, K);
+  a.magicS = magic_div(p.S);
+  a.magicM = magic_div(M);
   a.ws_part = nullptr;
   a.ws_cnt = nullptr;
   a.silu = silu;
