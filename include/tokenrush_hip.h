@@ -207,7 +207,8 @@ int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* strea
 /* ---------------------------------------------------------------- GDN (gated delta rule) step */
 
 /* Bytes of the workspace tr_gdn_step needs for M tokens, H key heads and HV value heads (0 if
- * unsupported). Zero-filled once by the caller; every call leaves its counters at zero. */
+ * unsupported; HV <= 256). Zero-filled once by the caller; every call leaves its counters at zero,
+ * which sit at a fixed offset, so one buffer sized for the largest call serves calls of every shape. */
 size_t tr_gdn_workspace_bytes(int M, int H, int HV);
 
 /* One M-token (1..8) GDN step of one layer: causal conv (kernel 4) over the ring with silu, b/a gates

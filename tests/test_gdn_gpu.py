@@ -141,3 +141,41 @@ def test_gdn_step_rejects_bad_shapes(dev):
     with pytest.raises(RuntimeError):
         gdn_step_fused(qkvz, x, w["ba_w"], ring, w["conv_w"], w["A"], w["dt_bias"], rec, one, w["norm_w"], one, CFG,
                        1e-6)
+
+
+def test_workspace_shared_by_calls_of_different_shapes(dev):
+    """One zero-filled workspace serves calls with different head counts in any order: the
+    arrival counters sit at a fixed place, so a small call's head outputs never land on a larger
+    call's counters (the step of the small hybrid, then the full-size head count)."""
+    from tokenrush_amd import gdn as gmod
+    print("gdn workspace shared across shapes", flush=True)
+    small = GDNConfig(512, 2, 4, K, V)
+    for cfg, seed in ((small, 1), (CFG, 2), (small, 3), (CFG, 4)):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        Hs, HVs, hid = cfg.gdn_k_heads, cfg.gdn_v_heads, cfg.hidden
+        C = 2 * Hs * K + HVs * V
+        M, pos, slot = 8, 21, 0
+        qkvz = torch.randn(M, C + HVs * V, device=dev, generator=gen).to(torch.bfloat16)
+        x = torch.randn(M, hid, device=dev, generator=gen).to(torch.bfloat16)
+        ba = (torch.randn(2 * HVs, hid, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        ring = torch.randn(C, RING, device=dev, generator=gen).to(torch.bfloat16)
+        conv = (torch.randn(C, 4, device=dev, generator=gen) * 0.3).to(torch.bfloat16)
+        A = -torch.exp(torch.randn(HVs, device=dev, generator=gen))
+        dt = torch.randn(HVs, device=dev, generator=gen)
+        nw = (torch.randn(V, device=dev, generator=gen) * 0.5 + 1).to(torch.bfloat16)
+        rec = torch.randn(8, HVs, K, V, device=dev, generator=gen) * 0.1
+        want = o.gdn_step(_np(qkvz), _np(x), _np(ba), _np(ring), _np(conv), _np(A), _np(dt), _np(rec), slot, _np(nw),
+                           pos, Hs, HVs, K, V, 1e-6)[0]
+        y = gdn_step_fused(qkvz, x, ba, ring, conv, A, dt, rec, torch.tensor([slot], device=dev), nw,
+                           torch.tensor([pos], device=dev), cfg, 1e-6)
+        torch.cuda.synchronize()
+        got = _np(y)
+        assert np.isfinite(got).all(), (HVs, seed)
+        assert np.linalg.norm(got - want) <= 5e-3 * np.linalg.norm(want), (HVs, seed)
+        assert gmod.workspace(M, Hs, HVs, dev).numel() >= _lib_ws(M, Hs, HVs)
+
+
+def _lib_ws(M, H, HV):
+    from tokenrush_amd import _lib
+    return int(_lib.lib().tr_gdn_workspace_bytes(M, H, HV))

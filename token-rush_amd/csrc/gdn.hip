@@ -366,14 +366,17 @@ using namespace tr;
 
 extern "C" {
 
-// Workspace: HV arrival counters (one per 128-byte line), the head outputs [M, HV V] fp32,
-// normalised q | k [M, 2 H K] fp32, the v conv outputs [M, HV V] bf16 and the gates [M, 2 HV]
-// fp32, each 256-byte aligned.
+// Workspace: kGdnMaxHV arrival counters (one per 128-byte line) in a fixed region at offset 0,
+// then the head outputs [M, HV V] fp32, normalised q | k [M, 2 H K] fp32, the v conv outputs
+// [M, HV V] bf16 and the gates [M, 2 HV] fp32, each 256-byte aligned. The counters' place does
+// not depend on the call's shape, so one zero-filled buffer serves calls of every shape (a
+// shape-dependent layout let one shape's head outputs land on another shape's counters).
+constexpr int kGdnMaxHV = 256;
 static size_t gdn_ws_part(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
 size_t tr_gdn_workspace_bytes(int M, int H, int HV) {
-  if (M < 1 || M > kGdnMaxM || H < 1 || HV < 1) return 0;
-  return gdn_ws_part((size_t)HV * 32 * sizeof(int)) + gdn_ws_part((size_t)M * HV * kGdnV * sizeof(float)) +
+  if (M < 1 || M > kGdnMaxM || H < 1 || HV < 1 || HV > kGdnMaxHV) return 0;
+  return gdn_ws_part((size_t)kGdnMaxHV * 32 * sizeof(int)) + gdn_ws_part((size_t)M * HV * kGdnV * sizeof(float)) +
          gdn_ws_part((size_t)M * 2 * H * kGdnK * sizeof(float)) + gdn_ws_part((size_t)M * HV * kGdnV * 2) +
          gdn_ws_part((size_t)M * 2 * HV * sizeof(float));
 }
@@ -383,7 +386,8 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
                 const void* norm_w, const int64_t* pos, void* y, void* workspace, size_t workspace_bytes, int M,
                 int H, int HV, int K, int V, int hidden, int R, float eps, void* stream) {
   if (M == 0) return TR_OK;
-  if (M < 0 || M > kGdnMaxM || K != kGdnK || V != kGdnV || H < 1 || HV < H || HV % H || (2 * H * K) % kGdnThreads ||
+  if (M < 0 || M > kGdnMaxM || K != kGdnK || V != kGdnV || H < 1 || HV < H || HV > kGdnMaxHV || HV % H ||
+      (2 * H * K) % kGdnThreads ||
       hidden < 32 || hidden % 32 || R < M + 3)
     return TR_ERR_SHAPE;
   if (!qkvz || !x || !ba_w || !ring || !conv_w || !A || !dt_bias || !rec || !slot || !norm_w || !pos || !y ||
@@ -406,7 +410,7 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
   a.y = (uint16_t*)y;
   char* w = (char*)workspace;
   a.cnt = (int*)w;
-  w += gdn_ws_part((size_t)HV * 32 * sizeof(int));
+  w += gdn_ws_part((size_t)kGdnMaxHV * 32 * sizeof(int));
   a.o_ws = (float*)w;
   w += gdn_ws_part((size_t)M * HV * kGdnV * sizeof(float));
   a.qk = (float*)w;
