@@ -172,6 +172,40 @@ def accept_latency(torch, dev):
     return res
 
 
+def lm_head_accept(torch, dev, M=M_VERIFY, reps=8):
+    """The verify tail of config 5: the 248320x5120 int4 lm_head at M rows with the accept, as
+    (a) the greedy accept in the GEMM's epilogue, (b) the GEMM writing logits followed by the
+    sampled accept kernel (temperature 1, top_p 0.95, top_k 64). Microseconds per call over a
+    graph of back-to-back calls (launch gaps included)."""
+    from tokenrush_amd.accept import AcceptState, accept_sampled, lm_head_greedy
+    from tokenrush_amd.quant import QLinear
+    from tokenrush_amd.sample import SamplingParams
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    K = 5120
+    q = torch.randint(0, 256, (V, K // 2), dtype=torch.uint8, device=dev, generator=gen)
+    s = (torch.rand(V, K // 128, device=dev, generator=gen) * 0.018 + 0.002).to(torch.bfloat16)
+    m = (torch.rand(V, K // 128, device=dev, generator=gen) * 0.14 - 0.15).to(torch.bfloat16)
+    lm = QLinear(q, s, m)
+    del q, s, m
+    hidden = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+    spec = torch.randint(0, V, (M,), device=dev, generator=gen)
+    u = torch.rand(M, device=dev, generator=gen)
+    p = SamplingParams(dev)
+    p.set(temperature=1.0, top_p=0.95, top_k=64)
+    st = AcceptState(M, dev)
+    cases = {"greedy_fused": lambda: lm_head_greedy(lm, hidden, spec, st, keep_logits=True),
+             "sampled": lambda: accept_sampled(lm(hidden), spec, p, st, u)}
+    out = {}
+    for name, fn in cases.items():
+        g = graph_of(torch, lambda fn=fn: [fn() for _ in range(reps)])
+        out[name] = round(timed_graph(torch, g) / reps * 1e6, 2)
+        del g
+    del lm
+    torch.cuda.empty_cache()
+    return out
+
+
 def config5_step(torch, dev, M=M_VERIFY, reps=10):
     """benchmark config 5: one verify step of the random-init 64-layer hybrid (48 GDN + 16 attention
     layers, int4 g128 weights, GDN steps and FP8 attention over 8192 live tokens) + lm_head + greedy
@@ -248,7 +282,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer verify-step graph (config 5)")
-    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config1"],
+    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config1", "lm_head"],
                     help="profiling aid: run just this projection's launches (M=8), or the config-5 step graph, and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: run a plain 1 GiB device copy (read 1 GiB, write 1 GiB) and exit")
@@ -269,6 +303,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
+    if a.only == "lm_head":
+        print(json.dumps({"lm_head_accept_us_m8": lm_head_accept(torch, dev)}))
         return
     if a.only == "config1":
         print(json.dumps({"config1_gemv_m1": config1_gemv(torch, gfx950, dev)}))
@@ -308,6 +345,7 @@ def main():
     del copies
     torch.cuda.empty_cache()
     c1 = config1_gemv(torch, gfx950, dev)
+    lmh = lm_head_accept(torch, dev)
     torch.cuda.empty_cache()
     c5 = None if a.no_config5 else config5_step(torch, dev)
 
@@ -346,6 +384,7 @@ def main():
                              "residual_m8": round(sum(k8.values()) * 1e6 + acc["residual_m8"], 2),
                              "tree_m32": round(sweep.get(32, float("nan")) + acc["tree_m32"], 2)},
         "config1_gemv_m1": c1,
+        "lm_head_accept_us_m8": lmh,
         "config5_verify_step": c5,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
