@@ -206,7 +206,7 @@ int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* strea
 
 /* ---------------------------------------------------------------- GDN (gated delta rule) step */
 
-/* Bytes of the workspace tr_gdn_step needs for M tokens, H key heads and HV value heads (0 if
+/* Bytes of the workspace tr_gdn_step / tr_gdn_tree_step need for M tokens (up to 32), H key heads and HV value heads (0 if
  * unsupported; HV <= 256). Zero-filled once by the caller; every call leaves its counters at zero,
  * which sit at a fixed offset, so one buffer sized for the largest call serves calls of every shape. */
 size_t tr_gdn_workspace_bytes(int M, int H, int HV);
@@ -227,9 +227,35 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
                 const void* norm_w, const int64_t* pos, void* y, void* workspace, size_t workspace_bytes, int M,
                 int H, int HV, int K, int V, int hidden, int R, float eps, void* stream);
 
+/* Draft-tree GDN step of one layer, M (1..32) nodes with parent[t] < t (node 0 the root, the
+ * committed token; a parent outside 0..t-1 reads as the root). Node t continues from its parent's
+ * state (the root from slot *slot) and writes its own to rec slot t; its conv window is its three
+ * nearest ancestors' inputs, with the ring's committed positions where the root path is shorter.
+ * The ring is only read: the nodes' conv inputs go to node_in [M, 2 H K + HV V] bf16 for
+ * tr_gdn_tree_commit. Every node's y equals a chain step over its root path. Other arguments as
+ * tr_gdn_step (R >= 3); the workspace is tr_gdn_workspace_bytes(M, H, HV).
+ * No counterpart in the reference (its trees were simulated on the host, bench/tree_accept.py:91-100);
+ * the per-node arithmetic is gdn_step_fused's (tokenrush/fused.py:119-236). */
+int tr_gdn_tree_step(const void* qkvz, int ld, const void* x, const void* ba_w, const void* ring, const void* conv_w,
+                     const float* A, const float* dt_bias, float* rec, long slot_stride, const int64_t* slot,
+                     const void* norm_w, const int64_t* pos, const int32_t* parent, void* node_in, void* y,
+                     void* workspace, size_t workspace_bytes, int M, int H, int HV, int K, int V, int hidden, int R,
+                     float eps, void* stream);
+
+/* Tree commit of the conv rings of `layers` GDN layers (ring [C, R] bf16 every ring_stride
+ * elements, node_in [M, C] bf16 every node_stride elements): ring column (base + d) % R <-
+ * node_in[commit[d]] for d = 0..n in order, base = *pos - n - 1 (pos, n_accepted and commit as
+ * tr_accept_tree leaves them), so each ring ends as a chain step over the accepted path leaves it.
+ * A path outside 0..M-1 or of M or more drafts commits nothing and sets *status (optional) to 1.
+ * No counterpart in the reference (chain commits are the position advance, model.py:376-382). */
+int tr_gdn_tree_commit(void* ring, long ring_stride, const void* node_in, long node_stride, int layers, int C, int R,
+                       int M, const int64_t* pos, const int64_t* n_accepted, const int64_t* commit, int32_t* status,
+                       void* stream);
+
 /* ---------------------------------------------------------------- attention over an FP8 KV cache */
 
-/* Bytes of the split-partials workspace of tr_attn_decode (0 if unsupported). */
+/* Bytes of the split-partials workspace of tr_attn_decode / tr_attn_decode_tree (M up to 32; 0 if
+ * unsupported). */
 size_t tr_attn_workspace_bytes(int M, int HQ, int nsplit);
 
 /* Prep of M (1..8) new tokens of one attention layer: q and k RMSNorm with (1 + w) gain, partial
@@ -244,11 +270,29 @@ int tr_attn_prep(const void* qkv, int ld, const void* q_norm_w, const void* k_no
 
 /* Flash-decoding of M (1..8) query tokens over cache rows 0..*pos + M - 1 (query t sees rows
  * <= *pos + t): nsplit key-range splits (two launches: split, then combine + sigmoid output gate
- * from qkv) -> out [M, HQ D] bf16. (HQ / HKV) * M <= 64, D == 256.
+ * from qkv) -> out [M, HQ D] bf16. D == 256.
  * Replaces: attn_decode_fused (tokenrush/fused.py:355-470: _attn_split_kernel + _attn_reduce_kernel). */
 int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, const void* v_cache,
                    const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos, void* out,
                    void* workspace, size_t workspace_bytes, int M, int HQ, int HKV, int D, int nsplit, void* stream);
+
+/* Draft-tree prep, M (1..32) nodes with parent[t] < t: as tr_attn_prep, but node t is roped at
+ * position *pos + depth(t) (where its root path puts it once committed) while its key and value go
+ * to cache row *pos + t (tr_commit_rows later moves the accepted path's rows into place).
+ * No counterpart in the reference; the per-node arithmetic is attn_prep's (tokenrush/fused.py:247-325). */
+int tr_attn_prep_tree(const void* qkv, int ld, const void* q_norm_w, const void* k_norm_w, const void* cos,
+                      const void* sin, int rotary_dim, const int64_t* pos, const int32_t* parent, void* k_cache,
+                      void* v_cache, float* k_scale, float* v_scale, int maxlen, void* q_out, int M, int HQ, int HKV,
+                      int D, float eps, void* stream);
+
+/* Draft-tree flash-decoding, M (1..32) nodes: node t sees the committed rows < *pos and the new
+ * rows *pos + i of its ancestors and itself (the ancestor mask). Otherwise as tr_attn_decode; the
+ * query rows of a kv head run in groups of 64, one more grid dimension.
+ * No counterpart in the reference; the per-node arithmetic is attn_decode_fused's (tokenrush/fused.py:355-470). */
+int tr_attn_decode_tree(const void* q, const void* qkv, int ld, const void* k_cache, const void* v_cache,
+                        const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos,
+                        const int32_t* parent, void* out, void* workspace, size_t workspace_bytes, int M, int HQ,
+                        int HKV, int D, int nsplit, void* stream);
 
 #ifdef __cplusplus
 }

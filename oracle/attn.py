@@ -15,6 +15,10 @@ Functions (reference file:line):
                               (running max per block, l summed before the value scale, P rounded to
                               bf16 after the scale), splits combined by their maxima, bf16(o) times
                               bf16(sigmoid(gate)).
+  attn_tree                -- no reference counterpart (the reference verifies chains only): by
+                              definition node t of a draft tree attends as the last query of a chain
+                              over its root path (rows pos .. pos + depth), prepped at those
+                              positions; its key and value rows land at row pos + t.
 
 Pinning (tests/test_oracle_attn.py):
   fp8_encode / fp8_decode  -- torch CPU float8_e4m3fn casts (a library routine): all 256 codes and
@@ -24,6 +28,8 @@ Pinning (tests/test_oracle_attn.py):
   attn_decode              -- a float64 softmax attention over the dequantised cache (the causal
                               rule written directly); independence of the split count; causality
                               (keys past pos + t do not change query t).
+  attn_tree                -- built from attn_prep / attn_decode by its definition; a chain tree
+                              reduces it to them.
 """
 import numpy as np
 
@@ -160,3 +166,27 @@ def attn_decode(q, qkv, k_cache, v_cache, k_scale, v_scale, pos: int, HQ: int, H
                 gs = bf16_round((F32(1) / (F32(1) + np.exp(-gate))).astype(F32))
                 out[t, hq * D:(hq + 1) * D] = bf16_round((o[t * G + g] * gs).astype(F32))
     return out
+
+
+def attn_tree(qkv, q_norm_w, k_norm_w, cos, sin, pos: int, parent, k_cache, v_cache, k_scale, v_scale, HQ: int,
+              HKV: int, D: int, RD: int, eps: float, nsplit: int = 32):
+    """Draft-tree prep + decode: node t is the last query of a chain over its root path. Returns
+    (out [M, HQ D], q [M, HQ, D], k_cache, v_cache, k_scale, v_scale) with node t's key and value
+    at row pos + t (roped at pos + depth(t))."""
+    from .gdn import root_path
+    qkv = np.asarray(qkv, F32)
+    M = qkv.shape[0]
+    kc, vc = np.array(k_cache, np.uint8, copy=True), np.array(v_cache, np.uint8, copy=True)
+    ks, vs = np.array(k_scale, F32, copy=True), np.array(v_scale, F32, copy=True)
+    out = np.empty((M, HQ * D), F32)
+    q = np.empty((M, HQ, D), F32)
+    for t in range(M):
+        p = root_path(parent, t)
+        d = len(p) - 1
+        qp, kp, vp, ksp, vsp = attn_prep(qkv[p], q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_cache, k_scale, v_scale,
+                                         HQ, HKV, D, RD, eps)
+        out[t] = attn_decode(qp, qkv[p], kp, vp, ksp, vsp, pos, HQ, HKV, D, nsplit)[-1]
+        q[t] = qp[-1]
+        kc[:, pos + t], vc[:, pos + t] = kp[:, pos + d], vp[:, pos + d]
+        ks[:, pos + t], vs[:, pos + t] = ksp[:, pos + d], vsp[:, pos + d]
+    return out, q, kc, vc, ks, vs

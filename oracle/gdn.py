@@ -15,6 +15,12 @@ Functions (reference file:line):
                     the state after every token into slot t, o = q^T S, gated RMSNorm.
   gated_rmsnorm  -- ops.py:10-19 and fused.py:196-204: bf16(o) normalised in fp32, cast, plain
                     gain in bf16, times silu(z) in fp32, cast.
+  gdn_tree_step  -- no reference counterpart (the reference verifies chains only; its trees were a
+                    host simulation, bench/tree_accept.py:91-100): by definition, node t of a draft
+                    tree is gdn_step over its root path (root = node 0 at position pos), so its
+                    output and state are that chain's last; the ring is not written.
+  tree_commit    -- the ring a gdn_step over the accepted path would leave: columns
+                    (pos + d) % R <- the path's conv inputs, d = 0..n (state.py:30-39 ring rule).
 
 Pinning (tests/test_oracle_gdn.py):
   gdn_step       -- (1) a float64 restatement of the single-token update in the reference's
@@ -28,6 +34,8 @@ Pinning (tests/test_oracle_gdn.py):
                     position 0) after many steps that wrap the ring.
   gates          -- float64 dot products (a library routine) before the bf16 rounding.
   gated_rmsnorm  -- torch CPU restatement of ops.gated_rmsnorm (the reference's dtype order).
+  gdn_tree_step  -- built from gdn_step (pinned above) by its definition; a chain tree
+  tree_commit       (parent[t] = t - 1) reduces both to one gdn_step, bit for bit.
 """
 import numpy as np
 
@@ -124,3 +132,40 @@ def gdn_step(qkvz, x, ba_w, ring, conv_w, A, dt_bias, rec, slot: int, norm_w, po
         z = qkvz[t, C:].reshape(HV, V)
         y[t] = gated_rmsnorm(o, norm_w, z, eps).reshape(-1)
     return y, ring, rec
+
+
+# ------------------------------------------------------------------ draft trees
+
+def root_path(parent, t: int) -> list:
+    """Node indices root..t of a draft tree (parent[t] < t, node 0 the root)."""
+    path = [int(t)]
+    while path[-1] > 0:
+        path.append(int(parent[path[-1]]))
+    return path[::-1]
+
+
+def gdn_tree_step(qkvz, x, ba_w, ring, conv_w, A, dt_bias, rec, slot: int, norm_w, pos: int, parent, H: int, HV: int,
+                  K: int, V: int, eps: float):
+    """Draft-tree step: node t is gdn_step over its root path. Returns (y [M, HV V], rec with
+    slot t = node t's state; the ring is unchanged)."""
+    qkvz, x = np.asarray(qkvz, F32), np.asarray(x, F32)
+    M = qkvz.shape[0]
+    rec0 = np.array(rec, F32, copy=True)
+    out_rec = rec0.copy()
+    y = np.empty((M, HV * V), F32)
+    for t in range(M):
+        p = root_path(parent, t)
+        yp, _, rp = gdn_step(qkvz[p], x[p], ba_w, ring, conv_w, A, dt_bias, rec0, slot, norm_w, pos, H, HV, K, V, eps)
+        y[t] = yp[-1]
+        out_rec[t] = rp[len(p) - 1]
+    return y, out_rec
+
+
+def tree_commit(ring, node_in, path, pos: int):
+    """ring [C, R] after the accept of `path` (node indices root..best) whose root sat at pos;
+    node_in [M, C] the nodes' conv inputs -> the new ring."""
+    ring = np.array(ring, F32, copy=True)
+    R = ring.shape[1]
+    for d, node in enumerate(path):
+        ring[:, (pos + d) % R] = np.asarray(node_in, F32)[node]
+    return ring

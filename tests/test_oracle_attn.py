@@ -136,3 +136,50 @@ def test_decode_split_count_independent():
     a = o.attn_decode(q, qkv, kc, vc, ks, vs, pos, HQ, HKV, D, nsplit=1)
     b = o.attn_decode(q, qkv, kc, vc, ks, vs, pos, HQ, HKV, D, nsplit=32)
     assert np.linalg.norm(a - b) <= 1e-2 * np.linalg.norm(a)
+
+
+def _rope_tab(maxlen):
+    ang = np.arange(maxlen)[:, None] * (1e7 ** -(np.arange(0, RD, 2) / RD))[None, :]
+    emb = np.concatenate([ang, ang], 1)
+    return bf16_round(np.cos(emb).astype(F32)), bf16_round(np.sin(emb).astype(F32))
+
+
+def test_tree_on_a_chain_is_the_chain_step():
+    """A chain tree reduces the tree oracle to attn_prep + attn_decode: bit for bit with one
+    split (masked keys add exact zeros, so the longer key range changes nothing)."""
+    rng = np.random.default_rng(11)
+    M, pos, maxlen = 5, 90, 128
+    qkv = _bf(rng, M, HQ * 2 * D + 2 * HKV * D)
+    qw, kw = _bf(rng, D, std=0.5), _bf(rng, D, std=0.5)
+    cos, sin = _rope_tab(maxlen)
+    kc, vc, ks, vs = _cache(rng, maxlen, pos)
+    q, kc2, vc2, ks2, vs2 = o.attn_prep(qkv, qw, kw, cos, sin, pos, kc, vc, ks, vs, HQ, HKV, D, RD, 1e-6)
+    out = o.attn_decode(q, qkv, kc2, vc2, ks2, vs2, pos, HQ, HKV, D, nsplit=1)
+    parent = np.arange(-1, M - 1, dtype=np.int32)
+    ot, qt, kct, vct, kst, vst = o.attn_tree(qkv, qw, kw, cos, sin, pos, parent, kc, vc, ks, vs, HQ, HKV, D, RD, 1e-6,
+                                             nsplit=1)
+    assert np.array_equal(out, ot) and np.array_equal(q, qt)
+    assert np.array_equal(kc2, kct) and np.array_equal(vc2, vct) and np.array_equal(ks2, kst)
+
+
+def test_tree_rows_and_masks():
+    """Node t's key row sits at pos + t, roped at pos + depth(t); its output does not depend on
+    nodes off its root path."""
+    rng = np.random.default_rng(12)
+    pos, maxlen = 70, 128
+    parent = np.array([-1, 0, 0, 1, 2, 3], np.int32)   # two branches: 0-1-3-5 and 0-2-4
+    M = parent.shape[0]
+    qkv = _bf(rng, M, HQ * 2 * D + 2 * HKV * D)
+    qw, kw = _bf(rng, D, std=0.5), _bf(rng, D, std=0.5)
+    cos, sin = _rope_tab(maxlen)
+    kc, vc, ks, vs = _cache(rng, maxlen, pos)
+    out, q, kct, vct, kst, vst = o.attn_tree(qkv, qw, kw, cos, sin, pos, parent, kc, vc, ks, vs, HQ, HKV, D, RD, 1e-6)
+    # node 4 (depth 2): its key equals a prep of its row at position pos + 2
+    _, k1, _, s1, _ = o.attn_prep(qkv[4:5], qw, kw, cos, sin, pos + 2, kc, vc, ks, vs, HQ, HKV, D, RD, 1e-6)
+    assert np.array_equal(kct[:, pos + 4], k1[:, pos + 2]) and np.array_equal(kst[:, pos + 4], s1[:, pos + 2])
+    q2 = qkv.copy()
+    q2[[2, 4]] = _bf(rng, 2, HQ * 2 * D + 2 * HKV * D)         # the other branch
+    out2 = o.attn_tree(q2, qw, kw, cos, sin, pos, parent, kc, vc, ks, vs, HQ, HKV, D, RD, 1e-6)[0]
+    for t in (0, 1, 3, 5):
+        assert np.array_equal(out2[t], out[t])
+    assert not np.array_equal(out2[4], out[4])

@@ -151,3 +151,42 @@ def test_multi_token_step_equals_single_steps():
         assert np.array_equal(yt[0], y[t])
         assert np.array_equal(rec[0], rec_m[t])
     assert np.array_equal(ring, ring_m)
+
+
+def test_tree_step_on_a_chain_is_the_chain_step():
+    """A chain tree (parent[t] = t - 1) reduces the tree oracle to gdn_step, bit for bit; the
+    commit of the whole path leaves the ring the chain step leaves."""
+    rng = np.random.default_rng(7)
+    w = _layer(rng)
+    rec0 = (rng.standard_normal((8, HV, K, V)) * 0.1).astype(F32)
+    ring0 = _bf(rng, C, R)
+    M, pos, slot = 6, 21, 3
+    qkvz, x = _bf(rng, M, C + HV * V), _bf(rng, M, HID)
+    args = (w["ba_w"], ring0, w["conv_w"], w["A"], w["dt_bias"], rec0, slot, w["norm_w"], pos)
+    y, ring_c, rec_c = o.gdn_step(qkvz, x, *args, H, HV, K, V, 1e-6)
+    parent = np.arange(-1, M - 1, dtype=np.int32)
+    yt, rec_t = o.gdn_tree_step(qkvz, x, *args, parent, H, HV, K, V, 1e-6)
+    assert np.array_equal(y, yt)
+    assert np.array_equal(rec_c[:M], rec_t[:M])
+    assert np.array_equal(o.tree_commit(ring0, qkvz[:, :C], list(range(M)), pos), ring_c)
+
+
+def test_tree_branches_do_not_see_each_other():
+    """Two children of the root: each one's output is the two-token chain [root, child], whatever
+    the sibling holds."""
+    rng = np.random.default_rng(8)
+    w = _layer(rng)
+    rec0 = (rng.standard_normal((8, HV, K, V)) * 0.1).astype(F32)
+    ring0 = _bf(rng, C, R)
+    pos, slot = 9, 0
+    qkvz, x = _bf(rng, 3, C + HV * V), _bf(rng, 3, HID)
+    args = (w["ba_w"], ring0, w["conv_w"], w["A"], w["dt_bias"], rec0, slot, w["norm_w"], pos)
+    parent = np.array([-1, 0, 0], np.int32)
+    y, rec = o.gdn_tree_step(qkvz, x, *args, parent, H, HV, K, V, 1e-6)
+    for child in (1, 2):
+        yc, _, rc = o.gdn_step(qkvz[[0, child]], x[[0, child]], *args, H, HV, K, V, 1e-6)
+        assert np.array_equal(y[child], yc[1]) and np.array_equal(rec[child], rc[1])
+    q2 = qkvz.copy()
+    q2[2] = _bf(rng, C + HV * V)
+    y2, _ = o.gdn_tree_step(q2, x, *args, parent, H, HV, K, V, 1e-6)
+    assert np.array_equal(y2[1], y[1]) and not np.array_equal(y2[2], y[2])

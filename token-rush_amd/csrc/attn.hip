@@ -27,7 +27,8 @@ namespace tr {
 
 constexpr int kAttnD = 256;      // head dim
 constexpr int kAttnBlk = 32;     // keys per LDS block
-constexpr int kAttnMaxM = 8;     // query tokens per step
+constexpr int kAttnMaxM = 8;     // query tokens per chain step
+constexpr int kAttnMaxTree = 32; // query tokens (nodes) per draft-tree step: one bit each in a mask word
 constexpr int kAttnWaves = 4;
 constexpr int kKPitch = kAttnD + 8;     // bf16 elements per K row in LDS
 constexpr int kVPitch = kAttnBlk + 4;   // bf16 elements per V^T row (one d) in LDS
@@ -97,19 +98,35 @@ struct AttnPrepArgs {
   float* k_scale;        // [HKV, maxlen]
   float* v_scale;
   uint16_t* q_out;       // [M, HQ, D] bf16
+  const int32_t* parent; // [M] draft-tree parents, or null for a chain
   int HQ, HKV, RD, maxlen, ld;
   float eps;
 };
 
-// One wave per (head, token); lane l holds dims 4 l .. 4 l + 3.
+// Parent of node t of a draft tree (parent[t] < t; node 0 is the root). A parent outside
+// 0..t-1 reads as the root, so every walk up the tree ends within t steps.
+__device__ __forceinline__ int attn_tree_parent(const int32_t* parent, int t) {
+  const int p = parent[t];
+  return (p >= 0 && p < t) ? p : 0;
+}
+
+// One wave per (head, token); lane l holds dims 4 l .. 4 l + 3. Token t is written to cache row
+// pos + t and roped at position pos + t, or, for node t of a draft tree, at pos + depth(t): the
+// position it takes once its root path is committed.
 __global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
   const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  int dep = t;
+  if (a.parent) {
+    dep = 0;
+    for (int j = t; j > 0 && dep < kAttnMaxTree; ++dep) j = attn_tree_parent(a.parent, j);
+  }
   // Positions past the cache's end: the rope table (maxlen rows) is read at the last row and no
   // cache row is written (the split kernel reads at most maxlen rows), so nothing outside the
   // cache is touched whatever the device position holds.
-  const int64_t p_raw = *a.pos + t;
+  const int64_t p_raw = *a.pos + t, r_raw = *a.pos + dep;
   const bool in_cache = p_raw >= 0 && p_raw < a.maxlen;
   const int64_t p = in_cache ? p_raw : (p_raw < 0 ? 0 : a.maxlen - 1);
+  const int64_t pr = r_raw < 0 ? 0 : (r_raw >= a.maxlen ? a.maxlen - 1 : r_raw);
   const bool isq = head < a.HQ;
   const int j = head - a.HQ;
   const uint16_t* row = a.qkv + (size_t)t * a.ld;
@@ -120,8 +137,8 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = (d0 + i) % (a.RD / 2);
-    cs_raw[i] = a.cos[(size_t)p * a.RD + r];
-    sn_raw[i] = a.sin[(size_t)p * a.RD + r];
+    cs_raw[i] = a.cos[(size_t)pr * a.RD + r];
+    sn_raw[i] = a.sin[(size_t)pr * a.RD + r];
   }
   float x[4], wv[4];
   {
@@ -206,6 +223,7 @@ struct AttnSplitArgs {
   float* m_part;           // [M HQ, NSPLIT]
   float* l_part;
   float* acc_part;         // [M HQ, NSPLIT, D]
+  const int32_t* parent;   // [M] draft-tree parents, or null for a chain
   int HQ, HKV, M, maxlen, nsplit;
   float scale;
 };
@@ -217,7 +235,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
   const int j = blockIdx.x / a.nsplit, s = blockIdx.x % a.nsplit;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = a.HQ / a.HKV;
-  const int rows = G * a.M;
+  const int rows = G * a.M - 16 * kAttnWaves * blockIdx.y;  // this workgroup's row group
   const int64_t pos = *a.pos;
   const int64_t L = pos + a.M;
   const int nblk = (int)((L + kAttnBlk - 1) / kAttnBlk);
@@ -228,14 +246,26 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
   // Q^T operand: lane l holds row 16 wave + l % 16, dims 8 (l / 16) + 32 jj .. + 7
   const int row = 16 * wave + (lane & 15);
   const bool rvalid = row < rows;
-  const int qi = rvalid ? row / G : 0;
-  const int hq = j * G + (rvalid ? row % G : 0);
+  const int grow = 16 * kAttnWaves * blockIdx.y + row;  // row of the kv head: query qi, head g
+  const int qi = rvalid ? grow / G : 0;
+  const int hq = j * G + (rvalid ? grow % G : 0);
   uint4 qb[8];
 #pragma unroll
   for (int jj = 0; jj < 8; ++jj)
     qb[jj] = rvalid ? *(const uint4*)(a.q + ((size_t)qi * a.HQ + hq) * kAttnD + 8 * (lane >> 4) + 32 * jj)
                     : make_uint4(0, 0, 0, 0);
-  const int64_t qlimit = pos + qi;
+  // The new keys query qi sees: rows pos + i for the bits i of vis -- i <= qi for a chain, the
+  // node's ancestors and itself for a tree.
+  uint32_t vis = qi >= 31 ? ~0u : (2u << qi) - 1u;
+  if (a.parent) {
+    vis = 0;
+    int jn = qi;
+    for (int d = 0; d < kAttnMaxTree; ++d) {
+      vis |= 1u << jn;
+      if (jn == 0) break;
+      jn = attn_tree_parent(a.parent, jn);
+    }
+  }
 
   f32x4 acc[16];
 #pragma unroll
@@ -334,7 +364,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t kidx = key0 + 16 * kt + 4 * (lane >> 4) + r;
-        const bool allowed = rvalid && kidx < L && kidx <= qlimit;
+        const bool allowed = rvalid && kidx < L && (kidx < pos || ((vis >> (int)(kidx - pos)) & 1u));
         const float v = allowed ? st[kt][r] * a.scale : -INFINITY;
         sc[4 * kt + r] = v;
         mx = fmaxf(mx, v);
@@ -448,18 +478,22 @@ using namespace tr;
 extern "C" {
 
 size_t tr_attn_workspace_bytes(int M, int HQ, int nsplit) {
-  if (M < 1 || M > kAttnMaxM || HQ < 1 || nsplit < 1) return 0;
+  if (M < 1 || M > kAttnMaxTree || HQ < 1 || nsplit < 1) return 0;
   const size_t rows = (size_t)M * HQ * nsplit;
   return rows * (2 + kAttnD) * sizeof(float);
 }
 
-int tr_attn_prep(const void* qkv, int ld, const void* q_norm_w, const void* k_norm_w, const void* cos,
-                 const void* sin, int rotary_dim, const int64_t* pos, void* k_cache, void* v_cache, float* k_scale,
-                 float* v_scale, int maxlen, void* q_out, int M, int HQ, int HKV, int D, float eps, void* stream) {
-  if (M == 0) return TR_OK;
+}  // extern "C"
+
+namespace {
+
+int attn_prep_launch(const void* qkv, int ld, const void* q_norm_w, const void* k_norm_w, const void* cos,
+                     const void* sin, int rotary_dim, const int64_t* pos, void* k_cache, void* v_cache, float* k_scale,
+                     float* v_scale, int maxlen, void* q_out, int M, int HQ, int HKV, int D, float eps,
+                     const int32_t* parent, void* stream) {
   // rotary_dim: a power of two (its two halves are then an xor-shuffle apart) in [8, D]
-  if (M < 0 || M > kAttnMaxM || D != kAttnD || HQ < 1 || HKV < 1 || HQ % HKV || (rotary_dim & (rotary_dim - 1)) ||
-      rotary_dim < 8 || rotary_dim > D || maxlen < M)
+  if (D != kAttnD || HQ < 1 || HKV < 1 || HQ % HKV || (rotary_dim & (rotary_dim - 1)) || rotary_dim < 8 ||
+      rotary_dim > D || maxlen < M)
     return TR_ERR_SHAPE;
   if (!qkv || !q_norm_w || !k_norm_w || !cos || !sin || !pos || !k_cache || !v_cache || !k_scale || !v_scale || !q_out)
     return TR_ERR_ARG;
@@ -476,6 +510,7 @@ int tr_attn_prep(const void* qkv, int ld, const void* q_norm_w, const void* k_no
   a.k_scale = k_scale;
   a.v_scale = v_scale;
   a.q_out = (uint16_t*)q_out;
+  a.parent = parent;
   a.HQ = HQ;
   a.HKV = HKV;
   a.RD = rotary_dim;
@@ -486,12 +521,11 @@ int tr_attn_prep(const void* qkv, int ld, const void* q_norm_w, const void* k_no
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
-int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, const void* v_cache,
-                   const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos, void* out,
-                   void* workspace, size_t workspace_bytes, int M, int HQ, int HKV, int D, int nsplit, void* stream) {
-  if (M == 0) return TR_OK;
-  if (M < 0 || M > kAttnMaxM || D != kAttnD || HQ < 1 || HKV < 1 || HQ % HKV || (HQ / HKV) * M > 16 * kAttnWaves ||
-      nsplit < 1 || nsplit > kMaxSplit || maxlen < M)
+int attn_decode_launch(const void* q, const void* qkv, int ld, const void* k_cache, const void* v_cache,
+                       const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos, void* out,
+                       void* workspace, size_t workspace_bytes, int M, int HQ, int HKV, int D, int nsplit,
+                       const int32_t* parent, void* stream) {
+  if (D != kAttnD || HQ < 1 || HKV < 1 || HQ % HKV || nsplit < 1 || nsplit > kMaxSplit || maxlen < M)
     return TR_ERR_SHAPE;
   if (!q || !qkv || !k_cache || !v_cache || !k_scale || !v_scale || !pos || !out || !workspace) return TR_ERR_ARG;
   if (ld < 2 * HQ * D + 2 * HKV * D || workspace_bytes < tr_attn_workspace_bytes(M, HQ, nsplit)) return TR_ERR_ARG;
@@ -506,13 +540,16 @@ int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, 
   s.m_part = (float*)workspace;
   s.l_part = s.m_part + rows;
   s.acc_part = s.l_part + rows;
+  s.parent = parent;
   s.HQ = HQ;
   s.HKV = HKV;
   s.M = M;
   s.maxlen = maxlen;
   s.nsplit = nsplit;
   s.scale = 1.f / sqrtf((float)D);
-  hipLaunchKernelGGL(attn_split_kernel, dim3(HKV * nsplit), dim3(64 * kAttnWaves), 0, (hipStream_t)stream, s);
+  // the G M query rows of a kv head in groups of 64 (one 16-row tile per wave)
+  const int groups = ((HQ / HKV) * M + 16 * kAttnWaves - 1) / (16 * kAttnWaves);
+  hipLaunchKernelGGL(attn_split_kernel, dim3(HKV * nsplit, groups), dim3(64 * kAttnWaves), 0, (hipStream_t)stream, s);
   if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
   AttnReduceArgs r;
   r.m_part = s.m_part;
@@ -525,6 +562,50 @@ int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, 
   r.ld = ld;
   hipLaunchKernelGGL(attn_reduce_kernel, dim3(M * HQ), dim3(kAttnD), 0, (hipStream_t)stream, r);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tr_attn_prep(const void* qkv, int ld, const void* q_norm_w, const void* k_norm_w, const void* cos,
+                 const void* sin, int rotary_dim, const int64_t* pos, void* k_cache, void* v_cache, float* k_scale,
+                 float* v_scale, int maxlen, void* q_out, int M, int HQ, int HKV, int D, float eps, void* stream) {
+  if (M == 0) return TR_OK;
+  if (M < 0 || M > kAttnMaxM) return TR_ERR_SHAPE;
+  return attn_prep_launch(qkv, ld, q_norm_w, k_norm_w, cos, sin, rotary_dim, pos, k_cache, v_cache, k_scale, v_scale,
+                          maxlen, q_out, M, HQ, HKV, D, eps, nullptr, stream);
+}
+
+int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, const void* v_cache,
+                   const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos, void* out,
+                   void* workspace, size_t workspace_bytes, int M, int HQ, int HKV, int D, int nsplit, void* stream) {
+  if (M == 0) return TR_OK;
+  if (M < 0 || M > kAttnMaxM) return TR_ERR_SHAPE;
+  return attn_decode_launch(q, qkv, ld, k_cache, v_cache, k_scale, v_scale, maxlen, pos, out, workspace,
+                            workspace_bytes, M, HQ, HKV, D, nsplit, nullptr, stream);
+}
+
+int tr_attn_prep_tree(const void* qkv, int ld, const void* q_norm_w, const void* k_norm_w, const void* cos,
+                      const void* sin, int rotary_dim, const int64_t* pos, const int32_t* parent, void* k_cache,
+                      void* v_cache, float* k_scale, float* v_scale, int maxlen, void* q_out, int M, int HQ, int HKV,
+                      int D, float eps, void* stream) {
+  if (M == 0) return TR_OK;
+  if (M < 0 || M > kAttnMaxTree) return TR_ERR_SHAPE;
+  if (!parent) return TR_ERR_ARG;
+  return attn_prep_launch(qkv, ld, q_norm_w, k_norm_w, cos, sin, rotary_dim, pos, k_cache, v_cache, k_scale, v_scale,
+                          maxlen, q_out, M, HQ, HKV, D, eps, parent, stream);
+}
+
+int tr_attn_decode_tree(const void* q, const void* qkv, int ld, const void* k_cache, const void* v_cache,
+                        const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos,
+                        const int32_t* parent, void* out, void* workspace, size_t workspace_bytes, int M, int HQ,
+                        int HKV, int D, int nsplit, void* stream) {
+  if (M == 0) return TR_OK;
+  if (M < 0 || M > kAttnMaxTree) return TR_ERR_SHAPE;
+  if (!parent) return TR_ERR_ARG;
+  return attn_decode_launch(q, qkv, ld, k_cache, v_cache, k_scale, v_scale, maxlen, pos, out, workspace,
+                            workspace_bytes, M, HQ, HKV, D, nsplit, parent, stream);
 }
 
 }  // extern "C"

@@ -41,9 +41,9 @@ constexpr int kGdnK = 128;   // key head dim
 constexpr int kGdnV = 128;   // value head dim
 constexpr int kGdnBV = 16;   // value columns per step workgroup: 2 per lane (8 column pairs x 8 row groups)
 constexpr int kGdnNVB = kGdnV / kGdnBV;
-constexpr int kGdnMaxM = 8;  // tokens per step (the reference's MP, fused.py:150)
+constexpr int kGdnMaxM = 8;  // tokens per chain step (the reference's MP, fused.py:150)
+constexpr int kGdnMaxTree = 32;  // nodes per draft-tree step
 constexpr int kGdnThreads = 256;
-static_assert(kGdnMaxM * kGdnBV <= kGdnThreads, "at most one v element per thread in the step prologue");
 static_assert(kGdnBV == 16, "the step kernel's lane layout: 8 column pairs");
 
 struct GdnArgs {
@@ -64,6 +64,8 @@ struct GdnArgs {
   float* qk;               // [M, 2 H K] fp32, workspace: normalised q (times K^-1/2) | k
   uint16_t* vconv;         // [M, HV V] bf16, workspace: conv + silu of the v channels
   float* gates;            // [M, 2 HV] fp32 (bf16 values), workspace: b | a
+  const int32_t* parent;   // [M] draft-tree parents, or null for a chain
+  uint16_t* node_in;       // [M, conv_dim] bf16: tree nodes' conv inputs (for the commit)
   long slot_stride;        // floats
   int ld, hidden, M, H, HV, R;
   float eps, scale;
@@ -76,11 +78,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gdn_rsrc(const void* p, size_t
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
 }
 
+// ------------------------------------------------------------------ tree helpers
+
+// Parent of node t of a draft tree (parent[t] < t; node 0 is the root). A parent outside
+// 0..t-1 reads as the root, so every walk up the tree ends within t steps.
+__device__ __forceinline__ int tree_parent(const int32_t* parent, int t) {
+  const int p = parent[t];
+  return (p >= 0 && p < t) ? p : 0;
+}
+
 // ------------------------------------------------------------------ prep: conv, norms, gates
 
+template <int MAXM>
 __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
-  __shared__ float part[4][kGdnMaxM];
-  __shared__ float ssq[4][kGdnMaxM];
+  __shared__ float part[4][8];
+  __shared__ float ssq[4][MAXM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = a.M;
   const int QK = a.H * kGdnK;
@@ -92,25 +104,84 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
     const int ch = blockIdx.x * kGdnThreads + tid;
     const bool on = ch < C;
     const int pr = (int)(*a.pos % a.R);  // ring column of token 0
-    float y[kGdnMaxM];
+    float y[MAXM];
 #pragma unroll
-    for (int t = 0; t < kGdnMaxM; ++t) y[t] = 0.f;
-    if (on) {
+    for (int t = 0; t < MAXM; ++t) y[t] = 0.f;
+    if (a.parent) {
+      // Draft tree: node t sits at depth d(t); its window is its three nearest ancestors' inputs,
+      // the committed positions pos + d - 3 .. pos - 1 (ring) standing in where the path is
+      // shorter. Inputs go to node_in for the commit; the ring is left as it is.
+      __shared__ uint16_t xs[MAXM][kGdnThreads];
+      __shared__ int anc[MAXM][3];  // ancestor 1..3 of node t: a node, or -(ring slot + 1)
+      if (tid < M) {
+        int j = tid, dep = 0;
+        for (int s = 0; s < MAXM && j > 0; ++s) {
+          j = tree_parent(a.parent, j);
+          ++dep;
+        }
+        j = tid;
+        for (int k = 0; k < 3; ++k) {  // k + 1 generations up
+          if (dep > k) {
+            j = tree_parent(a.parent, j);
+            anc[tid][k] = j;
+          } else {
+            anc[tid][k] = -(3 - (k + 1 - dep)) - 1;  // position pos - (k + 1 - dep): ring slot 3 - (k + 1 - dep)
+          }
+        }
+      }
+      float rw[3] = {0.f, 0.f, 0.f}, w[4] = {0.f, 0.f, 0.f, 0.f};
+      if (on) {
+        const uint2 wu = *(const uint2*)(a.conv_w + (size_t)ch * 4);
+        w[0] = bf16_bits_to_f32(wu.x & 0xFFFFu);
+        w[1] = bf16_bits_to_f32(wu.x >> 16);
+        w[2] = bf16_bits_to_f32(wu.y & 0xFFFFu);
+        w[3] = bf16_bits_to_f32(wu.y >> 16);
+        const uint16_t* rrow = a.ring + (size_t)ch * a.R;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) rw[j] = bf16_bits_to_f32(rrow[(pr + j - 3 + a.R) % a.R]);  // pos - 3 + j
+        for (int t = 0; t < M; ++t) {
+          const uint16_t xv = a.qkvz[(size_t)t * a.ld + ch];
+          xs[t][tid] = xv;
+          a.node_in[(size_t)t * C + ch] = xv;
+        }
+      }
+      __syncthreads();
+      if (on) {
+#pragma unroll
+        for (int t = 0; t < MAXM; ++t) {
+          if (t < M) {
+            float s[3];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+              const int an = anc[t][k];
+              s[k] = an >= 0 ? bf16_bits_to_f32(xs[an][tid]) : rw[-an - 1];
+            }
+            // window oldest first: ancestor 3, 2, 1, the node itself
+            float yv = s[2] * w[0];
+            yv = yv + s[1] * w[1];
+            yv = yv + s[0] * w[2];
+            yv = yv + bf16_bits_to_f32(xs[t][tid]) * w[3];
+            yv = bf16r(yv);
+            y[t] = bf16r(yv / (1.f + expf(-yv)));
+          }
+        }
+      }
+    } else if (on) {
       const uint2 wu = *(const uint2*)(a.conv_w + (size_t)ch * 4);
       const float w0 = bf16_bits_to_f32(wu.x & 0xFFFFu), w1 = bf16_bits_to_f32(wu.x >> 16);
       const float w2 = bf16_bits_to_f32(wu.y & 0xFFFFu), w3 = bf16_bits_to_f32(wu.y >> 16);
       uint16_t* rrow = a.ring + (size_t)ch * a.R;
-      float win[kGdnMaxM + 3];
-      uint16_t xin[kGdnMaxM];
+      float win[MAXM + 3];
+      uint16_t xin[MAXM];
 #pragma unroll
       for (int j = 0; j < 3; ++j) win[j] = bf16_bits_to_f32(rrow[(pr + j - 3 + a.R) % a.R]);
 #pragma unroll
-      for (int t = 0; t < kGdnMaxM; ++t) {
+      for (int t = 0; t < MAXM; ++t) {
         xin[t] = t < M ? a.qkvz[(size_t)t * a.ld + ch] : (uint16_t)0;
         win[t + 3] = bf16_bits_to_f32(xin[t]);
       }
 #pragma unroll
-      for (int t = 0; t < kGdnMaxM; ++t) {
+      for (int t = 0; t < MAXM; ++t) {
         if (t < M) {
           float yv = win[t] * w0;
           yv = yv + win[t + 1] * w1;
@@ -129,71 +200,81 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
     }
     // q or k: normalise each token's 128-channel head (waves 0-1: first head, 2-3: second)
 #pragma unroll
-    for (int t = 0; t < kGdnMaxM; ++t) {
+    for (int t = 0; t < MAXM; ++t) {
       const float s = sum_wave(y[t] * y[t]);
       if (lane == 0) ssq[wave][t] = s;
     }
     __syncthreads();
     const bool isq = ch < QK;
     const int hb = wave & ~1;  // first wave of this head
-    for (int t = 0; t < M; ++t) {
-      const float n = sqrtf((ssq[hb][t] + ssq[hb + 1][t]) + 1e-6f);
-      a.qk[(size_t)t * 2 * QK + ch] = isq ? y[t] / n * a.scale : y[t] / n;
+#pragma unroll
+    for (int t = 0; t < MAXM; ++t) {
+      if (t < M) {
+        const float n = sqrtf((ssq[hb][t] + ssq[hb + 1][t]) + 1e-6f);
+        a.qk[(size_t)t * 2 * QK + ch] = isq ? y[t] / n * a.scale : y[t] / n;
+      }
     }
     return;
   }
-  // gate row r of ba_w: b for r < HV, a for r >= HV
+  // gate row r of ba_w: b for r < HV, a for r >= HV; tokens in groups of 8
   const int r = blockIdx.x - n_conv;
   const int q0 = a.hidden / 4 * wave, q1 = a.hidden / 4 * (wave + 1);
   const auto xr = gdn_rsrc(a.x, (size_t)M * a.hidden * 2);
   const uint16_t* wrow = a.ba_w + (size_t)r * a.hidden;
-  float acc[kGdnMaxM];
-#pragma unroll
-  for (int t = 0; t < kGdnMaxM; ++t) acc[t] = 0.f;
-  // three 512-element chunks per pass (a quarter of hidden 5120 is 2.5), every load of a pass
-  // issued first; chunks past the quarter load zeros (offsets beyond the buffer resources)
   typedef uint32_t u4 __attribute__((ext_vector_type(4)));
   constexpr int kCh = 3;
   const auto wr = gdn_rsrc(wrow, (size_t)a.hidden * 2);
-  for (int e = q0 + 8 * lane; e < q1; e += kCh * 8 * 64) {
-    u4 wv[kCh], xv[kCh][kGdnMaxM];
+  for (int t0 = 0; t0 < M; t0 += 8) {
+    float acc[8];
 #pragma unroll
-    for (int c = 0; c < kCh; ++c) {
-      const int ec = e + c * 8 * 64;
-      const bool in = ec < q1;
-      wv[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, in ? ec * 2 : 0x7FFFFFF0, 0, 0);
+    for (int t = 0; t < 8; ++t) acc[t] = 0.f;
+    // three 512-element chunks per pass (a quarter of hidden 5120 is 2.5), every load of a pass
+    // issued first; chunks past the quarter load zeros (offsets beyond the buffer resources)
+    for (int e = q0 + 8 * lane; e < q1; e += kCh * 8 * 64) {
+      u4 wv[kCh], xv[kCh][8];
 #pragma unroll
-      for (int t = 0; t < kGdnMaxM; ++t)
-        xv[c][t] = __builtin_amdgcn_raw_buffer_load_b128(xr, (in && t < M) ? (t * a.hidden + ec) * 2 : 0x7FFFFFF0, 0, 0);
-    }
+      for (int c = 0; c < kCh; ++c) {
+        const int ec = e + c * 8 * 64;
+        const bool in = ec < q1;
+        wv[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, in ? ec * 2 : 0x7FFFFFF0, 0, 0);
 #pragma unroll
-    for (int c = 0; c < kCh; ++c) {
-      const uint32_t wa[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+        for (int t = 0; t < 8; ++t)
+          xv[c][t] = __builtin_amdgcn_raw_buffer_load_b128(xr, (in && t0 + t < M) ? ((t0 + t) * a.hidden + ec) * 2
+                                                                                   : 0x7FFFFFF0, 0, 0);
+      }
 #pragma unroll
-      for (int t = 0; t < kGdnMaxM; ++t) {
-        const uint32_t xw[4] = {xv[c][t].x, xv[c][t].y, xv[c][t].z, xv[c][t].w};
+      for (int c = 0; c < kCh; ++c) {
+        const uint32_t wa[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          acc[t] += bf16_bits_to_f32(xw[q] & 0xFFFFu) * bf16_bits_to_f32(wa[q] & 0xFFFFu) +
-                    bf16_bits_to_f32(xw[q] >> 16) * bf16_bits_to_f32(wa[q] >> 16);
+        for (int t = 0; t < 8; ++t) {
+          const uint32_t xw[4] = {xv[c][t].x, xv[c][t].y, xv[c][t].z, xv[c][t].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            acc[t] += bf16_bits_to_f32(xw[q] & 0xFFFFu) * bf16_bits_to_f32(wa[q] & 0xFFFFu) +
+                      bf16_bits_to_f32(xw[q] >> 16) * bf16_bits_to_f32(wa[q] >> 16);
+        }
       }
     }
-  }
+    __syncthreads();  // the previous group's part[] reads are done
 #pragma unroll
-  for (int t = 0; t < kGdnMaxM; ++t) {
-    const float v = sum_wave(acc[t]);
-    if (lane == 0) part[wave][t] = v;
+    for (int t = 0; t < 8; ++t) {
+      const float v = sum_wave(acc[t]);
+      if (lane == 0) part[wave][t] = v;
+    }
+    __syncthreads();
+    if (tid < 8 && t0 + tid < M)
+      a.gates[(size_t)(t0 + tid) * 2 * a.HV + r] = bf16r(((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid]);
   }
-  __syncthreads();
-  if (tid < M) a.gates[(size_t)tid * 2 * a.HV + r] = bf16r(((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid]);
 }
 
 // ------------------------------------------------------------------ step: the recurrence
 
+template <int MAXM>
 __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
-  __shared__ float cq[kGdnMaxM][kGdnK], ck[kGdnMaxM][kGdnK], cv[kGdnMaxM][kGdnBV];
-  __shared__ float beta_s[kGdnMaxM], decay_s[kGdnMaxM];
-  __shared__ float2 red[2][4][8], red_n[2][4][8];
+  __shared__ float cq[MAXM][kGdnK], ck[MAXM][kGdnK], cv[MAXM][kGdnBV];
+  __shared__ float beta_s[MAXM], decay_s[MAXM];
+  __shared__ int par_s[MAXM];
+  __shared__ float2 red[2][4][8], red_n[2][4][8], red_r[4][8];
   __shared__ int last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hv = blockIdx.x / kGdnNVB, vb = blockIdx.x % kGdnNVB;
@@ -216,7 +297,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   // q / k, v and the gates: every load issued at once (a loop with a runtime bound waited for
   // each iteration's loads); indices past M are clamped to token M - 1 and not stored
   {
-    constexpr int kQK = kGdnMaxM * kGdnK / kGdnThreads;  // 4
+    constexpr int kQK = MAXM * kGdnK / kGdnThreads;
     float qv[kQK], kv2[kQK];
 #pragma unroll
     for (int q = 0; q < kQK; ++q) {
@@ -224,8 +305,13 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
       qv[q] = a.qk[(size_t)t * 2 * QK + ih * kGdnK + c];
       kv2[q] = a.qk[(size_t)t * 2 * QK + QK + ih * kGdnK + c];
     }
-    const int ev = min(tid, kGdnMaxM * kGdnBV - 1), tv = min(ev / kGdnBV, M - 1), cvi = ev % kGdnBV;
-    const uint16_t vraw = a.vconv[(size_t)tv * VAL + hv * kGdnV + vb * kGdnBV + cvi];
+    constexpr int kVE = (MAXM * kGdnBV + kGdnThreads - 1) / kGdnThreads;  // v elements per thread
+    uint16_t vraw[kVE];
+#pragma unroll
+    for (int q = 0; q < kVE; ++q) {
+      const int ev = min(tid + kGdnThreads * q, MAXM * kGdnBV - 1), tv = min(ev / kGdnBV, M - 1);
+      vraw[q] = a.vconv[(size_t)tv * VAL + hv * kGdnV + vb * kGdnBV + ev % kGdnBV];
+    }
     const int tg = min(tid, M - 1);
     const float b = a.gates[(size_t)tg * 2 * a.HV + hv];
     const float av = a.gates[(size_t)tg * 2 * a.HV + a.HV + hv];
@@ -237,10 +323,15 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
         ck[t][c] = kv2[q];
       }
     }
-    if (tid < kGdnMaxM * kGdnBV && ev / kGdnBV < M) cv[ev / kGdnBV][cvi] = bf16_bits_to_f32(vraw);
+#pragma unroll
+    for (int q = 0; q < kVE; ++q) {
+      const int ev = tid + kGdnThreads * q;
+      if (ev < MAXM * kGdnBV && ev / kGdnBV < M) cv[ev / kGdnBV][ev % kGdnBV] = bf16_bits_to_f32(vraw[q]);
+    }
     if (tid < M) {
       beta_s[tid] = bf16r(1.f / (1.f + expf(-b)));
       decay_s[tid] = expf(a.A[hv] * softplus_f(av + a.dt_bias[hv]));
+      par_s[tid] = a.parent && tid > 0 ? tree_parent(a.parent, tid) : tid - 1;
     }
   }
   __syncthreads();
@@ -275,7 +366,33 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
     kv = wsum(p, 0);
   }
   float* const obase = a.o_ws + (size_t)hv * kGdnV + v0;
+  const size_t head_off = (size_t)hv * kGdnK * kGdnV + v0;
   for (int t = 0; t < M; ++t) {
+    if (t > 0 && par_s[t] != t - 1) {
+      // Draft tree, a node whose parent is not the previous node: continue from the parent's
+      // snapshot (this lane's own earlier stores) and sum its k_t product afresh. red_r is
+      // written only here; every such exchange is separated from the last by the barrier of a
+      // token exchange, so its reads are done before it is written again.
+      const float* src = a.rec + (size_t)par_s[t] * a.slot_stride + head_off;
+      float2 p = make_float2(0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        S[j] = *(const float2*)(src + (size_t)(k0 + j) * kGdnV);
+        const float kk = ck[t][k0 + j];
+        p.x += S[j].x * kk;
+        p.y += S[j].y * kk;
+      }
+      p = make_float2(ksum(p.x), ksum(p.y));
+      if (kg == 0) red_r[wave][vq] = p;
+      __syncthreads();
+      kv = red_r[0][vq];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float2 u = red_r[w][vq];
+        kv.x += u.x;
+        kv.y += u.y;
+      }
+    }
     const float beta = beta_s[t], eg = decay_s[t];
     const float* vt = &cv[t][c0];
     float2 dv;
@@ -283,7 +400,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
     dv.y = beta * (vt[1] - eg * kv.y);
     const int tn = min(t + 1, M - 1);  // the next token's k (the last token's sum is unused)
     float2 o = make_float2(0.f, 0.f), nx = o;
-    float* dst = a.rec + (size_t)t * a.slot_stride + (size_t)hv * kGdnK * kGdnV + v0;
+    float* dst = a.rec + (size_t)t * a.slot_stride + head_off;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float kk = ck[t][k0 + j], qq = cq[t][k0 + j], kn = ck[tn][k0 + j];
@@ -325,8 +442,10 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   // The last of the head's column blocks applies the gated norm to all V columns, every token.
   // Its z and gain loads are issued before the arrival count.
   const int Z = 2 * QK + VAL;
-  uint32_t zb[2][2];
-  for (int u = 0; u < 2; ++u) {
+  constexpr int kZU = MAXM / 4;  // tokens per wave in the norm
+  uint32_t zb[kZU][2];
+#pragma unroll
+  for (int u = 0; u < kZU; ++u) {
     const int t = wave + 4 * u;
     const uint16_t* zr = a.qkvz + (size_t)t * a.ld + Z + (size_t)hv * kGdnV;
     zb[u][0] = t < M ? zr[lane] : 0u;
@@ -343,7 +462,8 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   }
   __syncthreads();
   if (!last) return;
-  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+  for (int u = 0; u < kZU; ++u) {
     const int t = wave + 4 * u;
     if (t >= M) break;
     const float* op = a.o_ws + (size_t)t * VAL + (size_t)hv * kGdnV;
@@ -375,20 +495,25 @@ constexpr int kGdnMaxHV = 256;
 static size_t gdn_ws_part(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
 size_t tr_gdn_workspace_bytes(int M, int H, int HV) {
-  if (M < 1 || M > kGdnMaxM || H < 1 || HV < 1 || HV > kGdnMaxHV) return 0;
+  if (M < 1 || M > kGdnMaxTree || H < 1 || HV < 1 || HV > kGdnMaxHV) return 0;
   return gdn_ws_part((size_t)kGdnMaxHV * 32 * sizeof(int)) + gdn_ws_part((size_t)M * HV * kGdnV * sizeof(float)) +
          gdn_ws_part((size_t)M * 2 * H * kGdnK * sizeof(float)) + gdn_ws_part((size_t)M * HV * kGdnV * 2) +
          gdn_ws_part((size_t)M * 2 * HV * sizeof(float));
 }
 
-int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void* ring, const void* conv_w,
-                const float* A, const float* dt_bias, float* rec, long slot_stride, const int64_t* slot,
-                const void* norm_w, const int64_t* pos, void* y, void* workspace, size_t workspace_bytes, int M,
-                int H, int HV, int K, int V, int hidden, int R, float eps, void* stream) {
-  if (M == 0) return TR_OK;
-  if (M < 0 || M > kGdnMaxM || K != kGdnK || V != kGdnV || H < 1 || HV < H || HV > kGdnMaxHV || HV % H ||
-      (2 * H * K) % kGdnThreads ||
-      hidden < 32 || hidden % 32 || R < M + 3)
+}  // extern "C"
+
+namespace {
+
+// Shared by the chain and tree entry points: the shape checks past M, the workspace carve-up and
+// the two launches (8-token kernels up to M = 8, 32-token kernels above).
+int gdn_launch(const void* qkvz, int ld, const void* x, const void* ba_w, void* ring, const void* conv_w,
+               const float* A, const float* dt_bias, float* rec, long slot_stride, const int64_t* slot,
+               const void* norm_w, const int64_t* pos, void* y, void* workspace, size_t workspace_bytes, int M,
+               int H, int HV, int K, int V, int hidden, int R, float eps, const int32_t* parent, void* node_in,
+               void* stream) {
+  if (K != kGdnK || V != kGdnV || H < 1 || HV < H || HV > kGdnMaxHV || HV % H || (2 * H * K) % kGdnThreads ||
+      hidden < 32 || hidden % 32 || R < 3)
     return TR_ERR_SHAPE;
   if (!qkvz || !x || !ba_w || !ring || !conv_w || !A || !dt_bias || !rec || !slot || !norm_w || !pos || !y ||
       !workspace)
@@ -418,6 +543,8 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
   a.vconv = (uint16_t*)w;
   w += gdn_ws_part((size_t)M * HV * V * 2);
   a.gates = (float*)w;
+  a.parent = parent;
+  a.node_in = (uint16_t*)node_in;
   a.slot_stride = slot_stride;
   a.ld = ld;
   a.hidden = hidden;
@@ -428,10 +555,78 @@ int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void*
   a.eps = eps;
   a.scale = 1.f / sqrtf((float)K);
   const int C = 2 * H * K + HV * V;
-  hipLaunchKernelGGL(gdn_prep_kernel, dim3((C + kGdnThreads - 1) / kGdnThreads + 2 * HV), dim3(kGdnThreads), 0,
-                     (hipStream_t)stream, a);
-  if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
-  hipLaunchKernelGGL(gdn_step_kernel, dim3(HV * kGdnNVB), dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+  const dim3 prep_grid((C + kGdnThreads - 1) / kGdnThreads + 2 * HV), step_grid(HV * kGdnNVB);
+  if (M <= kGdnMaxM) {
+    hipLaunchKernelGGL(gdn_prep_kernel<kGdnMaxM>, prep_grid, dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+    if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
+    hipLaunchKernelGGL(gdn_step_kernel<kGdnMaxM>, step_grid, dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+  } else {
+    hipLaunchKernelGGL(gdn_prep_kernel<kGdnMaxTree>, prep_grid, dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+    if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
+    hipLaunchKernelGGL(gdn_step_kernel<kGdnMaxTree>, step_grid, dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+  }
+  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+// Tree commit of the conv rings: ring column (base + d) % R <- node_in[commit[d]] for the
+// accepted path d = 0..n in order (base = pos - n - 1, pos already advanced by the accept), so
+// the ring ends as a chain step over the path would leave it. One thread per (layer, channel).
+// A path that names a node outside 0..M-1 or is longer than M commits nothing and sets *status.
+__global__ void gdn_tree_commit_kernel(uint16_t* ring, long ring_stride, const uint16_t* node_in, long node_stride,
+                                       int layers, int C, int R, int M, const int64_t* pos,
+                                       const int64_t* n_accepted, const int64_t* commit, int* status) {
+  const int ch = blockIdx.x * blockDim.x + threadIdx.x, layer = blockIdx.y;
+  const int n = (int)*n_accepted;
+  const int64_t base = *pos - n - 1;
+  bool bad = n < 0 || n >= M || base < 0;
+  for (int d = 0; d <= n && d < M; ++d) bad |= commit[d] < 0 || commit[d] >= M;
+  if (bad) {
+    if (status && ch == 0 && layer == 0) *status = 1;
+    return;
+  }
+  if (ch >= C || layer >= layers) return;
+  uint16_t* rrow = ring + (size_t)layer * ring_stride + (size_t)ch * R;
+  const uint16_t* src = node_in + (size_t)layer * node_stride + ch;
+  for (int d = 0; d <= n; ++d) rrow[(base + d) % R] = src[(size_t)commit[d] * C];
+}
+
+}  // namespace
+
+extern "C" {
+
+int tr_gdn_step(const void* qkvz, int ld, const void* x, const void* ba_w, void* ring, const void* conv_w,
+                const float* A, const float* dt_bias, float* rec, long slot_stride, const int64_t* slot,
+                const void* norm_w, const int64_t* pos, void* y, void* workspace, size_t workspace_bytes, int M,
+                int H, int HV, int K, int V, int hidden, int R, float eps, void* stream) {
+  if (M == 0) return TR_OK;
+  if (M < 0 || M > kGdnMaxM || R < M + 3) return TR_ERR_SHAPE;
+  return gdn_launch(qkvz, ld, x, ba_w, ring, conv_w, A, dt_bias, rec, slot_stride, slot, norm_w, pos, y, workspace,
+                    workspace_bytes, M, H, HV, K, V, hidden, R, eps, nullptr, nullptr, stream);
+}
+
+int tr_gdn_tree_step(const void* qkvz, int ld, const void* x, const void* ba_w, const void* ring, const void* conv_w,
+                     const float* A, const float* dt_bias, float* rec, long slot_stride, const int64_t* slot,
+                     const void* norm_w, const int64_t* pos, const int32_t* parent, void* node_in, void* y,
+                     void* workspace, size_t workspace_bytes, int M, int H, int HV, int K, int V, int hidden, int R,
+                     float eps, void* stream) {
+  if (M == 0) return TR_OK;
+  if (M < 0 || M > kGdnMaxTree) return TR_ERR_SHAPE;
+  if (!parent || !node_in) return TR_ERR_ARG;
+  return gdn_launch(qkvz, ld, x, ba_w, const_cast<void*>(ring), conv_w, A, dt_bias, rec, slot_stride, slot, norm_w,
+                    pos, y, workspace, workspace_bytes, M, H, HV, K, V, hidden, R, eps, parent, node_in, stream);
+}
+
+int tr_gdn_tree_commit(void* ring, long ring_stride, const void* node_in, long node_stride, int layers, int C, int R,
+                       int M, const int64_t* pos, const int64_t* n_accepted, const int64_t* commit, int32_t* status,
+                       void* stream) {
+  if (layers == 0 || M == 0) return TR_OK;
+  if (layers < 0 || C < 1 || R < 1 || M < 1 || M > kGdnMaxTree || ring_stride < (long)C * R ||
+      node_stride < (long)M * C)
+    return TR_ERR_SHAPE;
+  if (!ring || !node_in || !pos || !n_accepted || !commit) return TR_ERR_ARG;
+  hipLaunchKernelGGL(gdn_tree_commit_kernel, dim3((C + 255) / 256, layers), dim3(256), 0, (hipStream_t)stream,
+                     (uint16_t*)ring, ring_stride, (const uint16_t*)node_in, node_stride, layers, C, R, M, pos,
+                     n_accepted, commit, (int*)status);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 

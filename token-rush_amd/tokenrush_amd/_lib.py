@@ -55,6 +55,12 @@ SIGNATURES = {
     "tr_attn_decode": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P]),
     "tr_gdn_step": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, ctypes.c_long, _P, _P, _P, _P, _P, _S, _I, _I, _I, _I,
                          _I, _I, _I, ctypes.c_float, _P]),
+    "tr_gdn_tree_step": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, ctypes.c_long, _P, _P, _P, _P, _P, _P, _P, _S, _I,
+                              _I, _I, _I, _I, _I, _I, ctypes.c_float, _P]),
+    "tr_gdn_tree_commit": (_I, [_P, ctypes.c_long, _P, ctypes.c_long, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "tr_attn_prep_tree": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I,
+                               ctypes.c_float, _P]),
+    "tr_attn_decode_tree": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P]),
 }
 
 _lib = None

@@ -53,9 +53,20 @@ def _check_cache(k_cache, v_cache, k_scale, v_scale, cfg):
             raise RuntimeError("attention: caches and scales must be contiguous")
 
 
-def attn_prep(qkv, q_norm_w, k_norm_w, cos, sin, pos_t, k_cache, v_cache, cfg, k_scale=None, v_scale=None):
+def _parent(parent, M, device):
+    if parent is None:
+        return None
+    if parent.dtype != torch.int32 or not parent.is_cuda or parent.device != device or parent.numel() < M:
+        raise RuntimeError("parent must be a device int32 tensor with one entry per node")
+    return parent.contiguous()
+
+
+def attn_prep(qkv, q_norm_w, k_norm_w, cos, sin, pos_t, k_cache, v_cache, cfg, k_scale=None, v_scale=None,
+              parent=None):
     """qkv [M, HQ 2D + 2 HKV D] bf16 -> q [M, HQ D] bf16, normed and roped; writes the new keys
-    and values into cache rows pos..pos+M-1 (fused.py:313-325)."""
+    and values into cache rows pos..pos+M-1 (fused.py:313-325). With parent (device int32 [M],
+    parent[t] < t, node 0 the root) the M <= 32 rows are the nodes of a draft tree: node t is
+    roped at pos + depth(t) and still written to row pos + t."""
     _lib.require_gpu(qkv, q_norm_w, k_norm_w, cos, sin, pos_t, k_cache, v_cache)
     _check_cache(k_cache, v_cache, k_scale, v_scale, cfg)
     if qkv.dtype != torch.bfloat16 or qkv.stride(1) != 1:
@@ -68,11 +79,15 @@ def attn_prep(qkv, q_norm_w, k_norm_w, cos, sin, pos_t, k_cache, v_cache, cfg, k
     HQ, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
     q = torch.empty(M, HQ * D, device=qkv.device, dtype=torch.bfloat16)
     ld = qkv.stride(0) if M > 1 else qkv.shape[1]
-    rc = _lib.lib().tr_attn_prep(_lib.ptr(qkv), ld, _lib.ptr(q_norm_w), _lib.ptr(k_norm_w), _lib.ptr(cos),
-                                 _lib.ptr(sin), cfg.rotary_dim, _lib.ptr(pos_t), _lib.ptr(k_cache), _lib.ptr(v_cache),
-                                 _lib.ptr(k_scale), _lib.ptr(v_scale), k_cache.shape[1], _lib.ptr(q), M, HQ, HKV, D,
-                                 float(cfg.eps), _lib.stream_of(qkv))
-    _lib.check(rc, "tr_attn_prep")
+    par = _parent(parent, M, qkv.device)
+    P = _lib.ptr
+    head = (P(qkv), ld, P(q_norm_w), P(k_norm_w), P(cos), P(sin), cfg.rotary_dim, P(pos_t))
+    tail = (P(k_cache), P(v_cache), P(k_scale), P(v_scale), k_cache.shape[1], P(q), M, HQ, HKV, D, float(cfg.eps),
+            _lib.stream_of(qkv))
+    if par is None:
+        _lib.check(_lib.lib().tr_attn_prep(*head, *tail), "tr_attn_prep")
+    else:
+        _lib.check(_lib.lib().tr_attn_prep_tree(*head, P(par), *tail), "tr_attn_prep_tree")
     return q
 
 
@@ -87,10 +102,12 @@ def workspace(M: int, HQ: int, nsplit: int, device):
     return _lib.grown_workspace(_ws, key, need, device, zero=False)
 
 
-def attn_decode_fused(q, qkv, k_cache, v_cache, pos_t, cfg, k_scale=None, v_scale=None, NSPLIT=NSPLIT):
+def attn_decode_fused(q, qkv, k_cache, v_cache, pos_t, cfg, k_scale=None, v_scale=None, NSPLIT=NSPLIT,
+                      parent=None):
     """q [M, HQ D] (from attn_prep) for the M new tokens at pos.., qkv [M, ..] (for the gates)
     -> gated attention output [M, HQ D] bf16; query t sees cache rows <= pos + t
-    (fused.py:448-470)."""
+    (fused.py:448-470). With parent (a draft tree of M <= 32 nodes, as attn_prep), node t sees
+    the rows before pos and the rows pos + i of its ancestors and itself."""
     _lib.require_gpu(q, qkv, k_cache, v_cache, pos_t)
     _check_cache(k_cache, v_cache, k_scale, v_scale, cfg)
     if q.dtype != torch.bfloat16 or not q.is_contiguous() or qkv.dtype != torch.bfloat16 or qkv.stride(1) != 1:
@@ -100,9 +117,12 @@ def attn_decode_fused(q, qkv, k_cache, v_cache, pos_t, cfg, k_scale=None, v_scal
     out = torch.empty(M, HQ * D, device=q.device, dtype=torch.bfloat16)
     ws = workspace(M, HQ, NSPLIT, q.device)
     ld = qkv.stride(0) if M > 1 else qkv.shape[1]
-    rc = _lib.lib().tr_attn_decode(_lib.ptr(q), _lib.ptr(qkv), ld, _lib.ptr(k_cache), _lib.ptr(v_cache),
-                                   _lib.ptr(k_scale), _lib.ptr(v_scale), k_cache.shape[1], _lib.ptr(pos_t),
-                                   _lib.ptr(out), _lib.ptr(ws), ws.numel(), M, HQ, HKV, D, NSPLIT,
-                                   _lib.stream_of(q))
-    _lib.check(rc, "tr_attn_decode")
+    par = _parent(parent, M, q.device)
+    P = _lib.ptr
+    head = (P(q), P(qkv), ld, P(k_cache), P(v_cache), P(k_scale), P(v_scale), k_cache.shape[1], P(pos_t))
+    tail = (P(out), P(ws), ws.numel(), M, HQ, HKV, D, NSPLIT, _lib.stream_of(q))
+    if par is None:
+        _lib.check(_lib.lib().tr_attn_decode(*head, *tail), "tr_attn_decode")
+    else:
+        _lib.check(_lib.lib().tr_attn_decode_tree(*head, P(par), *tail), "tr_attn_decode_tree")
     return out

@@ -23,6 +23,12 @@ kernels of this package:
     greedy accept: n_accepted, tok, pos += n + 1, slot = n (model.py:302-312), in the lm_head
     GEMM's epilogue (one launch)
 
+A draft-tree step (step_tree, benchmark config 4: up to 32 nodes) runs the same body with the
+tree mixers (ancestor-masked attention, per-node GDN states), then the tree accept and its commit:
+the accepted path's KV rows and scales move to consecutive positions, the conv rings take the
+path's inputs, and the slot names the deepest accepted node, whose state snapshot the next step
+continues from.
+
 The decode state (tokenrush/state.py:14-43) lives on the device: the position and the committed
 recurrent-state slot (read by the mixers, written by the accept), the conv rings and the fp32
 recurrent state in 8 snapshot slots per GDN layer, and the FP8 KV cache with per-(head, position)
@@ -35,12 +41,12 @@ from dataclasses import dataclass
 import torch
 
 from . import gfx950
-from .accept import AcceptState, accept_residual, accept_sampled, lm_head_greedy
+from .accept import AcceptState, accept_residual, accept_sampled, accept_tree, commit_rows, lm_head_greedy
 from .attn import AttnConfig, attn_decode_fused, attn_prep, rope_table
 from .attn import NSPLIT as ATTN_NSPLIT
 from .attn import workspace as attn_workspace
 from .fused import add_rmsnorm
-from .gdn import RING, GDNConfig, gdn_step_fused
+from .gdn import RING, GDNConfig, gdn_step_fused, tree_commit
 from .gdn import workspace as gdn_workspace
 from .quant import QLinear
 from .sample import SamplingParams
@@ -71,6 +77,7 @@ class StepConfig:
     live: int = 8192           # tokens already in the KV cache when the step runs
     headroom: int = 1024       # cache rows past `live` for the steps that follow
     layer_types: tuple = None  # a checkpoint's 'linear_attention' / 'full_attention' per layer
+    tree_nodes: int = 0        # > 0: room for draft-tree steps of up to this many nodes (<= 32)
 
     def is_attention(self, li: int) -> bool:
         if self.layer_types is not None:
@@ -104,6 +111,10 @@ class StepConfig:
     @property
     def maxlen(self) -> int:
         return self.live + self.headroom
+
+    @property
+    def n_slots(self) -> int:      # recurrent-state snapshots: one per verify row or tree node
+        return max(MAX_M, self.tree_nodes)
 
 
 SMALL = StepConfig(n_layers=4, hidden=512, mlp=1024, vocab=4096, gdn_k_heads=2, gdn_v_heads=4, n_heads=2,
@@ -193,16 +204,20 @@ class Layer:
 
 class StepState:
     """Decode state of the step (tokenrush/state.py:14-43) for the GDN and attention layers:
-    position and committed slot, conv rings, recurrent state in MAX_M snapshot slots, FP8 KV
-    cache with per-(head, position) scales; rows 0..live-1 of the cache hold random tokens."""
+    position and committed slot, conv rings, recurrent state in cfg.n_slots snapshot slots, FP8
+    KV cache with per-(head, position) scales; rows 0..live-1 of the cache hold random tokens.
+    With cfg.tree_nodes, node_in [n_gdn, tree_nodes, conv_dim] keeps a tree step's conv inputs
+    for the ring commit."""
 
     def __init__(self, cfg: StepConfig, n_gdn: int, n_attn: int, gen, device):
         g = cfg.gdn
         self.pos = torch.full((1,), cfg.live, dtype=torch.int64, device=device)
         self.slot = torch.zeros(1, dtype=torch.int64, device=device)
         self.ring = _bf16((n_gdn, g.conv_dim, RING), 1.0, gen, device)
-        self.rec = torch.randn(MAX_M, n_gdn, g.gdn_v_heads, g.gdn_k_dim, g.gdn_v_dim, device=device,
+        self.rec = torch.randn(cfg.n_slots, n_gdn, g.gdn_v_heads, g.gdn_k_dim, g.gdn_v_dim, device=device,
                                generator=gen) * 0.05
+        self.node_in = (torch.zeros(n_gdn, cfg.tree_nodes, g.conv_dim, dtype=torch.bfloat16, device=device)
+                        if cfg.tree_nodes else None)
         HKV, D, L = cfg.n_kv_heads, cfg.head_dim, cfg.maxlen
         self.k = torch.zeros(n_attn, HKV, L, D, dtype=torch.float8_e4m3fn, device=device)
         self.v = torch.zeros_like(self.k)
@@ -260,28 +275,33 @@ class VerifyModel:
     def nbytes(self) -> int:
         return self.lm_head.nbytes + sum(L.weight_bytes() for L in self.layers)
 
-    def mixer(self, li: int, L: Layer, n: torch.Tensor, pos_t, slot_t) -> torch.Tensor:
-        """The layer's token mixer: [M, hidden] normed input -> [M, mixer out] (model.py:76-121)."""
+    def mixer(self, li: int, L: Layer, n: torch.Tensor, pos_t, slot_t, parent=None) -> torch.Tensor:
+        """The layer's token mixer: [M, hidden] normed input -> [M, mixer out] (model.py:76-121);
+        with parent, the rows are the nodes of a draft tree."""
         cfg, st = self.cfg, self.state
         u = L.proj(n)
         if L.attention:
             a = self.attn_index[li]
             q = attn_prep(u, L.q_norm_w, L.k_norm_w, st.cos, st.sin, pos_t, st.k[a], st.v[a], cfg.attn,
-                          st.k_scale[a], st.v_scale[a])
-            return attn_decode_fused(q, u, st.k[a], st.v[a], pos_t, cfg.attn, st.k_scale[a], st.v_scale[a])
+                          st.k_scale[a], st.v_scale[a], parent=parent)
+            return attn_decode_fused(q, u, st.k[a], st.v[a], pos_t, cfg.attn, st.k_scale[a], st.v_scale[a],
+                                     parent=parent)
         g = self.gdn_index[li]
+        node_in = None if parent is None else st.node_in[g]
         return gdn_step_fused(u, n, L.in_ba, st.ring[g], L.conv_w, L.A, L.dt_bias, st.rec[:, g], slot_t, L.norm_w,
-                              pos_t, cfg.gdn, cfg.eps)
+                              pos_t, cfg.gdn, cfg.eps, parent=parent, node_in=node_in)
 
-    def hidden(self, x0: torch.Tensor, pos_t=None, slot_t=None) -> torch.Tensor:
+    def hidden(self, x0: torch.Tensor, pos_t=None, slot_t=None, parent=None) -> torch.Tensor:
         """x0 [M, hidden] bf16 -> post-final-norm hidden [M, hidden] bf16 (model.py:252-254)."""
         cfg = self.cfg
         pos_t = self.state.pos if pos_t is None else pos_t
         slot_t = self.state.slot if slot_t is None else slot_t
+        if parent is not None and (not cfg.tree_nodes or x0.shape[0] > cfg.tree_nodes):
+            raise RuntimeError(f"a {x0.shape[0]}-node tree step needs StepConfig(tree_nodes >= {x0.shape[0]})")
         x, h = x0, None
         for li, L in enumerate(self.layers):
             x, n = add_rmsnorm(x, h, L.ln1, cfg.eps)
-            h = L.out.partials(self.mixer(li, L, n, pos_t, slot_t))
+            h = L.out.partials(self.mixer(li, L, n, pos_t, slot_t, parent))
             x, n = add_rmsnorm(x, h, L.ln2, cfg.eps)
             h = L.down.partials(L.gate_up.silu_mul(n))
         _, n = add_rmsnorm(x, h, self.final_norm, cfg.eps)
@@ -331,6 +351,24 @@ class VerifyModel:
             accept_residual(logits, q, spec_toks, u, st)
         else:
             accept_sampled(logits, spec_toks, params, st, u)
+        return logits
+
+
+    def step_tree(self, x0: torch.Tensor, node_toks: torch.Tensor, parent: torch.Tensor,
+                  st: AcceptState) -> torch.Tensor:
+        """Draft-tree verify (benchmark config 4): x0 [M, hidden] the nodes' input rows, node_toks
+        [M] int64 (node 0 the committed token), parent [M] int32 device (parent[t] < t). The body
+        runs the tree mixers at st.pos / st.slot; the lm_head's logits [M, vocab] feed the tree
+        accept (the deepest root path whose every node equals its parent row's argmax), which
+        advances st.pos by n + 1 and sets st.slot to that path's last node; then the commit moves
+        the path's KV rows and scales to positions pos..pos+n and writes its conv inputs into the
+        rings. Returns the logits."""
+        S = self.state
+        logits = self.lm_head(self.hidden(x0, st.pos, st.slot, parent))
+        accept_tree(logits, node_toks, parent, st)
+        for cache, layout in ((S.k, "rows"), (S.v, "rows"), (S.k_scale, "scalars"), (S.v_scale, "scalars")):
+            commit_rows(cache, st, layout, max_n=x0.shape[0] - 1)
+        tree_commit(S.ring, S.node_in, st)
         return logits
 
 
