@@ -22,6 +22,8 @@ accept      on-device accept latency (benchmark config 3 and 4): mean per launch
 config5     one verify step of the random-init 64-layer hybrid at M = 8 (257 int4 GEMMs, split-K
             partial consumers, 48 GDN steps, 16 FP8 attention layers over 8192 live tokens, lm_head,
             greedy accept) captured as one hipGraph; time per replay and weight bytes / time.
+config4     a seeded 32-node draft tree verified through the same model (tree mixers, M = 32
+            GEMMs, lm_head, tree accept and commit), one hipGraph; time per replay.
 cpu_baseline  the reference's CPU path restated in torch (unpack, in-place dequant, F.linear) on
             one layer set at M = 8, OMP_NUM_THREADS host cores, median of >= 5 passes
             (about 10 s).
@@ -206,14 +208,15 @@ def lm_head_accept(torch, dev, M=M_VERIFY, reps=8):
     return out
 
 
-def config5_step(torch, dev, M=M_VERIFY, reps=10):
+def config5_step(torch, dev, M=M_VERIFY, reps=10, tree=True):
     """benchmark config 5: one verify step of the random-init 64-layer hybrid (48 GDN + 16 attention
     layers, int4 g128 weights, GDN steps and FP8 attention over 8192 live tokens) + lm_head + greedy
-    accept/commit, captured as one hipGraph (tokenrush_amd.step). Returns the replay time and the weight-streaming rate."""
+    accept/commit, captured as one hipGraph (tokenrush_amd.step). Returns the replay time and the
+    weight-streaming rate; with tree, also config 4 through the same model (config4_tree_step)."""
     from tokenrush_amd.accept import AcceptState
     from tokenrush_amd.step import StepConfig, VerifyModel, prepare
     t0 = time.perf_counter()
-    model = VerifyModel(StepConfig(), device=dev, seed=5)
+    model = VerifyModel(StepConfig(tree_nodes=32 if tree else 0), device=dev, seed=5)
     prepare(model, M)
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
@@ -231,9 +234,11 @@ def config5_step(torch, dev, M=M_VERIFY, reps=10):
     nbytes, state_bytes, live = model.nbytes(), model.state.nbytes(), model.cfg.live
     n_attn = sum(1 for li in range(model.cfg.n_layers) if model.cfg.is_attention(li))
     launches = (model.cfg.n_layers - n_attn) * 7 + n_attn * 9 + 2
-    del g, model
+    del g
+    c4 = config4_tree_step(torch, dev, model, reps=reps) if tree else None
+    del model
     torch.cuda.empty_cache()
-    return {"ms_per_step": round(t * 1e3, 3), "weights_GB": round(nbytes / 1e9, 3),
+    return c4, {"ms_per_step": round(t * 1e3, 3), "weights_GB": round(nbytes / 1e9, 3),
             "weight_GBps": round(nbytes / t / 1e9, 1), "launches": launches, "M": M, "replays": reps,
             "build_s": round(build_s, 1),
             "state_GB": round(state_bytes / 1e9, 3), "live_tokens": live,
@@ -241,6 +246,49 @@ def config5_step(torch, dev, M=M_VERIFY, reps=10):
                     "(split-K partial consumers), 48 GDN steps (conv ring, delta rule, 8 snapshot slots, gated norm), "
                     "16 attention layers (prep + FP8 flash-decoding split + combine) over 8192 live tokens, lm_head "
                     "248320x5120 with the greedy accept/commit in its epilogue"}
+
+
+def _random_parent(n, seed, max_branch=4, max_depth=7):
+    """A seeded draft tree: node 0 the root (-1); each later node hangs off a random earlier node
+    with fewer than max_branch children and depth below max_depth."""
+    import random
+    rng = random.Random(seed)
+    parent, depth, kids = [-1], [0], [0]
+    for i in range(1, n):
+        j = rng.choice([k for k in range(i) if kids[k] < max_branch and depth[k] < max_depth])
+        parent.append(j)
+        depth.append(depth[j] + 1)
+        kids.append(0)
+        kids[j] += 1
+    return parent
+
+
+def config4_tree_step(torch, dev, model, reps=10, M=32):
+    """benchmark config 4 through the config-5 model: a seeded 32-node draft tree (branching <= 4,
+    depth <= 7) verified by the 64-layer step with the tree mixers (ancestor-masked attention,
+    per-node GDN states), M = 32 GEMMs, lm_head, tree accept and commit (KV rows, scales, conv
+    rings), one hipGraph (VerifyModel.step_tree)."""
+    from tokenrush_amd.accept import AcceptState
+    from tokenrush_amd.step import prepare
+    prepare(model, M)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(8)
+    x0 = torch.randn(M, model.cfg.hidden, device=dev, generator=gen).to(torch.bfloat16)
+    toks = torch.randint(0, model.cfg.vocab, (M,), device=dev, generator=gen)
+    parent = torch.tensor(_random_parent(M, seed=4), dtype=torch.int32, device=dev)
+    st = AcceptState(M, dev)
+    st.pos.fill_(model.cfg.live)
+    st.slot.zero_()
+    g = graph_of(torch, lambda: model.step_tree(x0, toks, parent, st))
+    # each replay advances pos by the accepted depth + 1 <= 8
+    assert (reps + 3) * 8 <= model.cfg.headroom
+    st.pos.fill_(model.cfg.live)
+    t = timed_graph(torch, g, reps=reps)
+    del g
+    return {"ms_per_step": round(t * 1e3, 3), "M": M, "replays": reps,
+            "note": "one hipGraph: 257 int4 GEMMs at M=32, tree GDN steps (per-node state, 32 snapshot slots), "
+                    "ancestor-masked FP8 attention over 8192 live tokens, lm_head 248320x5120 writing logits, tree "
+                    "accept, commit of KV rows/scales (4 launches) and conv rings (1 launch)"}
 
 
 def cpu_baseline(M=M_VERIFY, min_reps=5, budget_s=10.0):
@@ -282,7 +330,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer verify-step graph (config 5)")
-    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config1", "lm_head"],
+    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config4", "config1", "lm_head"],
                     help="profiling aid: run just this projection's launches (M=8), or the config-5 step graph, and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: run a plain 1 GiB device copy (read 1 GiB, write 1 GiB) and exit")
@@ -310,8 +358,9 @@ def main():
     if a.only == "config1":
         print(json.dumps({"config1_gemv_m1": config1_gemv(torch, gfx950, dev)}))
         return
-    if a.only == "config5":
-        print(json.dumps({"config5_verify_step": config5_step(torch, dev, reps=max(1, a.steps // 30))}))
+    if a.only in ("config5", "config4"):
+        c4, c5 = config5_step(torch, dev, reps=max(1, a.steps // 30), tree=a.only == "config4")
+        print(json.dumps({"config5_verify_step": c5, "config4_tree_step": c4}))
         return
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
@@ -347,7 +396,7 @@ def main():
     c1 = config1_gemv(torch, gfx950, dev)
     lmh = lm_head_accept(torch, dev)
     torch.cuda.empty_cache()
-    c5 = None if a.no_config5 else config5_step(torch, dev)
+    c4, c5 = (None, None) if a.no_config5 else config5_step(torch, dev)
 
     value = step_bytes[8] * a.steps / wall8 / 1e9
     gu = dict((n, (N, K)) for n, N, K, _ in LAYER_SET)["gate_up"]
@@ -386,6 +435,7 @@ def main():
         "config1_gemv_m1": c1,
         "lm_head_accept_us_m8": lmh,
         "config5_verify_step": c5,
+        "config4_tree_step": c4,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "int4_gemm_kernel gate_up 34816x5120 M=8 (%.2f us)" % (k8["gate_up"] * 1e6), **busy},

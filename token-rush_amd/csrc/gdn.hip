@@ -21,9 +21,9 @@
 //
 // Two launches on MI355X:
 //   gdn_prep_kernel does the work every column block of a head shares, once: the conv of all
-//   channels for the M tokens (one thread per channel; the ring update), the L2 normalisation
-//   of q and k (a 256-channel workgroup holds two whole heads), and the gate dot products
-//   (one workgroup per gate row, the four waves splitting the hidden dim).
+//   channels (one thread per channel, a workgroup per 8 tokens, 4 in trees over 8 nodes; the ring update),
+//   the L2 normalisation of q and k (a 256-channel workgroup holds two whole heads), and the gate dot products
+//   (one workgroup per gate row and group of 8 tokens, the four waves splitting the hidden dim).
 //   gdn_step_kernel runs the recurrence, one workgroup of four waves per (value head, 16-column
 //   block): 48 x 8 = 384 workgroups, so the M x 64 KB-per-head snapshot stores -- the kernel's
 //   cost -- spread over every CU. Wave w holds rows 32 w .. 32 w + 31 of the block's [128 x 16]
@@ -33,6 +33,13 @@
 //   steps) and the 4 waves (LDS, fixed order), once per token for both o_t and kv_{t+1}.
 //   The gated norm needs the whole head: the four blocks store bf16 o with agent-scope stores,
 //   and the last of them to arrive normalizes the head for every token.
+//
+// Draft trees (tr_gdn_tree_step, up to 32 nodes, parent[t] < t): node t is the last token of a
+// chain over its root path. The conv window is the node's three nearest ancestors (the ring's
+// committed columns where the path is shorter); the ring is not written, the nodes' inputs go to
+// node_in and tr_gdn_tree_commit writes the accepted path's into the ring. In the recurrence a
+// node whose parent is not the previous node continues from the parent's snapshot, loaded during
+// the previous node's work, so every node still costs one cross-wave exchange.
 #include "accept_common.h"
 
 namespace tr {
@@ -43,6 +50,8 @@ constexpr int kGdnBV = 16;   // value columns per step workgroup: 2 per lane (8 
 constexpr int kGdnNVB = kGdnV / kGdnBV;
 constexpr int kGdnMaxM = 8;  // tokens per chain step (the reference's MP, fused.py:150)
 constexpr int kGdnMaxTree = 32;  // nodes per draft-tree step
+// tokens per conv workgroup of the prep: all of a chain step's, 4 of a larger tree's
+template <int MAXM> constexpr int gdn_tg() { return MAXM <= 8 ? 8 : 4; }
 constexpr int kGdnThreads = 256;
 static_assert(kGdnBV == 16, "the step kernel's lane layout: 8 column pairs");
 
@@ -66,6 +75,7 @@ struct GdnArgs {
   float* gates;            // [M, 2 HV] fp32 (bf16 values), workspace: b | a
   const int32_t* parent;   // [M] draft-tree parents, or null for a chain
   uint16_t* node_in;       // [M, conv_dim] bf16: tree nodes' conv inputs (for the commit)
+  int* tinfo;              // [3, 32] workspace: the tree's processing order, depths, branch flags
   long slot_stride;        // floats
   int ld, hidden, M, H, HV, R;
   float eps, scale;
@@ -87,144 +97,183 @@ __device__ __forceinline__ int tree_parent(const int32_t* parent, int t) {
   return (p >= 0 && p < t) ? p : 0;
 }
 
+// The order the recurrence visits a tree's nodes in: depth first, children by index (each node
+// right after its parent or after the subtree of an earlier sibling), computed by threads
+// 0..M-1 of one workgroup. Node t's position is depth(t) plus, for every node a != root on its
+// root path, the sizes of a's earlier siblings' subtrees. Writes order[32] | depth[32] | branch
+// flags[32] (1 for a node with two or more children: its state is visited again) to info.
+__device__ void tree_order(const int32_t* parent, int M, int* info) {
+  __shared__ int tp[32], tsz[32], tesz[32];
+  __shared__ uint32_t tanc[32];
+  const int t = threadIdx.x;
+  const bool node = t < M;
+  if (node) tp[t] = t == 0 ? -1 : tree_parent(parent, t);
+  __syncthreads();
+  int dep = 0;
+  uint32_t anc = node ? 1u << t : 0u;
+  if (node)
+    for (int j = t; j > 0; ++dep) {
+      j = tp[j];
+      anc |= 1u << j;
+    }
+  if (node) tanc[t] = anc;
+  __syncthreads();
+  int size = 0, kids = 0;
+  if (node)
+    for (int u = 0; u < M; ++u) {
+      size += (tanc[u] >> t) & 1u;
+      kids += tp[u] == t;
+    }
+  if (node) tsz[t] = size;
+  __syncthreads();
+  int esz = 0;
+  if (node && t > 0)
+    for (int u = 1; u < t; ++u) esz += tp[u] == tp[t] ? tsz[u] : 0;
+  if (node) tesz[t] = esz;
+  __syncthreads();
+  if (node) {
+    int pre = dep;
+    for (uint32_t m = anc & ~1u; m; m &= m - 1) pre += tesz[__builtin_ctz(m)];
+    info[pre] = t;
+    info[32 + t] = dep;
+    info[64 + t] = kids >= 2;
+  }
+}
+
 // ------------------------------------------------------------------ prep: conv, norms, gates
 
 template <int MAXM>
 __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
+  constexpr int TG = gdn_tg<MAXM>();
   __shared__ float part[4][8];
-  __shared__ float ssq[4][MAXM];
+  __shared__ float ssq[4][TG];
+  __shared__ int src_s[MAXM][3];  // window inputs of token t, 1..3 back: a token, or -(ring slot + 1)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = a.M;
   const int QK = a.H * kGdnK;
   const int C = 2 * QK + a.HV * kGdnV;
-  const int n_conv = (C + kGdnThreads - 1) / kGdnThreads;
+  const int n_cb = (C + kGdnThreads - 1) / kGdnThreads;
+  const int n_conv = n_cb * ((M + TG - 1) / TG);
+  if (a.parent && blockIdx.x == gridDim.x - 1) {
+    tree_order(a.parent, M, a.tinfo);
+    return;
+  }
   if ((int)blockIdx.x < n_conv) {
-    // one conv channel per thread; a workgroup's 256 channels are two whole q or k heads (QK is
-    // a multiple of 256) or 256 v channels
-    const int ch = blockIdx.x * kGdnThreads + tid;
+    // One conv channel per thread for TG tokens; a workgroup's 256 channels are two whole q or
+    // k heads (QK is a multiple of 256) or 256 v channels. The window of token t holds the inputs
+    // 1..3 back on its path: the previous tokens of a chain, a tree node's ancestors, and the
+    // ring's committed positions pos - 1 .. pos - 3 where the path is shorter.
+    const int cb = blockIdx.x % n_cb, t0 = TG * (blockIdx.x / n_cb);
+    const int ch = cb * kGdnThreads + tid;
     const bool on = ch < C;
     const int pr = (int)(*a.pos % a.R);  // ring column of token 0
-    float y[MAXM];
-#pragma unroll
-    for (int t = 0; t < MAXM; ++t) y[t] = 0.f;
-    if (a.parent) {
-      // Draft tree: node t sits at depth d(t); its window is its three nearest ancestors' inputs,
-      // the committed positions pos + d - 3 .. pos - 1 (ring) standing in where the path is
-      // shorter. Inputs go to node_in for the commit; the ring is left as it is.
-      __shared__ uint16_t xs[MAXM][kGdnThreads];
-      __shared__ int anc[MAXM][3];  // ancestor 1..3 of node t: a node, or -(ring slot + 1)
-      if (tid < M) {
-        int j = tid, dep = 0;
-        for (int s = 0; s < MAXM && j > 0; ++s) {
+    if (a.parent && tid < M) {
+      int j = tid, dep = 0;
+      for (int s = 0; s < MAXM && j > 0; ++s) {
+        j = tree_parent(a.parent, j);
+        ++dep;
+      }
+      j = tid;
+      for (int k = 0; k < 3; ++k) {  // k + 1 back
+        if (dep > k) {
           j = tree_parent(a.parent, j);
-          ++dep;
-        }
-        j = tid;
-        for (int k = 0; k < 3; ++k) {  // k + 1 generations up
-          if (dep > k) {
-            j = tree_parent(a.parent, j);
-            anc[tid][k] = j;
-          } else {
-            anc[tid][k] = -(3 - (k + 1 - dep)) - 1;  // position pos - (k + 1 - dep): ring slot 3 - (k + 1 - dep)
-          }
+          src_s[tid][k] = j;
+        } else {
+          src_s[tid][k] = -(3 - (k + 1 - dep)) - 1;  // position pos - (k + 1 - dep): ring slot 3 - (k + 1 - dep)
         }
       }
-      float rw[3] = {0.f, 0.f, 0.f}, w[4] = {0.f, 0.f, 0.f, 0.f};
-      if (on) {
-        const uint2 wu = *(const uint2*)(a.conv_w + (size_t)ch * 4);
-        w[0] = bf16_bits_to_f32(wu.x & 0xFFFFu);
-        w[1] = bf16_bits_to_f32(wu.x >> 16);
-        w[2] = bf16_bits_to_f32(wu.y & 0xFFFFu);
-        w[3] = bf16_bits_to_f32(wu.y >> 16);
-        const uint16_t* rrow = a.ring + (size_t)ch * a.R;
+    }
+    if (a.parent) __syncthreads();
+    float y[TG];
 #pragma unroll
-        for (int j = 0; j < 3; ++j) rw[j] = bf16_bits_to_f32(rrow[(pr + j - 3 + a.R) % a.R]);  // pos - 3 + j
-        for (int t = 0; t < M; ++t) {
-          const uint16_t xv = a.qkvz[(size_t)t * a.ld + ch];
-          xs[t][tid] = xv;
-          a.node_in[(size_t)t * C + ch] = xv;
-        }
-      }
-      __syncthreads();
-      if (on) {
-#pragma unroll
-        for (int t = 0; t < MAXM; ++t) {
-          if (t < M) {
-            float s[3];
-#pragma unroll
-            for (int k = 0; k < 3; ++k) {
-              const int an = anc[t][k];
-              s[k] = an >= 0 ? bf16_bits_to_f32(xs[an][tid]) : rw[-an - 1];
-            }
-            // window oldest first: ancestor 3, 2, 1, the node itself
-            float yv = s[2] * w[0];
-            yv = yv + s[1] * w[1];
-            yv = yv + s[0] * w[2];
-            yv = yv + bf16_bits_to_f32(xs[t][tid]) * w[3];
-            yv = bf16r(yv);
-            y[t] = bf16r(yv / (1.f + expf(-yv)));
-          }
-        }
-      }
-    } else if (on) {
+    for (int u = 0; u < TG; ++u) y[u] = 0.f;
+    if (on) {
       const uint2 wu = *(const uint2*)(a.conv_w + (size_t)ch * 4);
       const float w0 = bf16_bits_to_f32(wu.x & 0xFFFFu), w1 = bf16_bits_to_f32(wu.x >> 16);
       const float w2 = bf16_bits_to_f32(wu.y & 0xFFFFu), w3 = bf16_bits_to_f32(wu.y >> 16);
       uint16_t* rrow = a.ring + (size_t)ch * a.R;
-      float win[MAXM + 3];
-      uint16_t xin[MAXM];
+      // every load first: the ring's committed inputs, the tokens' own and (trees) the windows'
+      float win[TG + 3];  // chain: positions pos - 3 .. pos + TG - 1
+      uint16_t xin[TG], wt[TG][3];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) win[j] = bf16_bits_to_f32(rrow[(pr + j - 3 + a.R) % a.R]);
+      for (int j = 0; j < 3; ++j) win[j] = bf16_bits_to_f32(rrow[(pr + j - 3 + a.R) % a.R]);  // pos - 3 + j
 #pragma unroll
-      for (int t = 0; t < MAXM; ++t) {
-        xin[t] = t < M ? a.qkvz[(size_t)t * a.ld + ch] : (uint16_t)0;
-        win[t + 3] = bf16_bits_to_f32(xin[t]);
+      for (int u = 0; u < TG; ++u) {
+        const int t = min(t0 + u, M - 1);
+        xin[u] = a.qkvz[(size_t)t * a.ld + ch];
+        win[u + 3] = bf16_bits_to_f32(t0 + u < M ? xin[u] : (uint16_t)0);
+        if (a.parent)
+#pragma unroll
+          for (int k = 0; k < 3; ++k) {
+            const int sn = src_s[t][k];
+            wt[u][k] = sn >= 0 ? a.qkvz[(size_t)sn * a.ld + ch] : (uint16_t)0;
+          }
       }
 #pragma unroll
-      for (int t = 0; t < MAXM; ++t) {
+      for (int u = 0; u < TG; ++u) {
+        const int t = t0 + u;
         if (t < M) {
-          float yv = win[t] * w0;
-          yv = yv + win[t + 1] * w1;
-          yv = yv + win[t + 2] * w2;
-          yv = yv + win[t + 3] * w3;
+          // oldest first: 3 back, 2 back, 1 back, the token itself (a chain's group starts at
+          // token 0, so its window is win[u .. u + 3])
+          float sv[3] = {win[u + 2], win[u + 1], win[u]};
+          if (a.parent)
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+              const int sn = src_s[t][k];
+              sv[k] = sn >= 0 ? bf16_bits_to_f32(wt[u][k]) : win[-sn - 1];
+            }
+          float yv = sv[2] * w0;
+          yv = yv + sv[1] * w1;
+          yv = yv + sv[0] * w2;
+          yv = yv + bf16_bits_to_f32(xin[u]) * w3;
           yv = bf16r(yv);
-          y[t] = bf16r(yv / (1.f + expf(-yv)));
+          y[u] = bf16r(yv / (1.f + expf(-yv)));
         }
       }
-      for (int t = 0; t < M; ++t) rrow[(pr + t) % a.R] = xin[t];
+      if (a.parent) {  // a tree's inputs wait for the commit
+#pragma unroll
+        for (int u = 0; u < TG; ++u)
+          if (t0 + u < M) a.node_in[(size_t)(t0 + u) * C + ch] = xin[u];
+      } else {  // a chain's go to the ring, after every read of it
+#pragma unroll
+        for (int u = 0; u < TG; ++u)
+          if (t0 + u < M) rrow[(pr + t0 + u) % a.R] = xin[u];
+      }
     }
-    if ((int)blockIdx.x * kGdnThreads >= 2 * QK) {  // v channels: stored as they are
+    if (cb * kGdnThreads >= 2 * QK) {  // v channels: stored as they are
       if (on)
-        for (int t = 0; t < M; ++t) a.vconv[(size_t)t * a.HV * kGdnV + (ch - 2 * QK)] = f32_to_bf16_bits(y[t]);
+#pragma unroll
+        for (int u = 0; u < TG; ++u)
+          if (t0 + u < M) a.vconv[(size_t)(t0 + u) * a.HV * kGdnV + (ch - 2 * QK)] = f32_to_bf16_bits(y[u]);
       return;
     }
     // q or k: normalise each token's 128-channel head (waves 0-1: first head, 2-3: second)
 #pragma unroll
-    for (int t = 0; t < MAXM; ++t) {
-      const float s = sum_wave(y[t] * y[t]);
-      if (lane == 0) ssq[wave][t] = s;
+    for (int u = 0; u < TG; ++u) {
+      const float sq = sum_wave(y[u] * y[u]);
+      if (lane == 0) ssq[wave][u] = sq;
     }
     __syncthreads();
     const bool isq = ch < QK;
     const int hb = wave & ~1;  // first wave of this head
 #pragma unroll
-    for (int t = 0; t < MAXM; ++t) {
-      if (t < M) {
-        const float n = sqrtf((ssq[hb][t] + ssq[hb + 1][t]) + 1e-6f);
-        a.qk[(size_t)t * 2 * QK + ch] = isq ? y[t] / n * a.scale : y[t] / n;
+    for (int u = 0; u < TG; ++u) {
+      if (t0 + u < M) {
+        const float n = sqrtf((ssq[hb][u] + ssq[hb + 1][u]) + 1e-6f);
+        a.qk[(size_t)(t0 + u) * 2 * QK + ch] = isq ? y[u] / n * a.scale : y[u] / n;
       }
     }
     return;
   }
-  // gate row r of ba_w: b for r < HV, a for r >= HV; tokens in groups of 8
-  const int r = blockIdx.x - n_conv;
+  // gate row r of ba_w (b for r < HV, a for r >= HV) for one group of 8 tokens
+  const int r = (blockIdx.x - n_conv) % (2 * a.HV), t0 = 8 * ((blockIdx.x - n_conv) / (2 * a.HV));
   const int q0 = a.hidden / 4 * wave, q1 = a.hidden / 4 * (wave + 1);
   const auto xr = gdn_rsrc(a.x, (size_t)M * a.hidden * 2);
   const uint16_t* wrow = a.ba_w + (size_t)r * a.hidden;
   typedef uint32_t u4 __attribute__((ext_vector_type(4)));
   constexpr int kCh = 3;
   const auto wr = gdn_rsrc(wrow, (size_t)a.hidden * 2);
-  for (int t0 = 0; t0 < M; t0 += 8) {
+  {
     float acc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = 0.f;
@@ -255,7 +304,6 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
         }
       }
     }
-    __syncthreads();  // the previous group's part[] reads are done
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const float v = sum_wave(acc[t]);
@@ -269,12 +317,12 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
 
 // ------------------------------------------------------------------ step: the recurrence
 
-template <int MAXM>
+template <int MAXM, bool TREE>
 __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   __shared__ float cq[MAXM][kGdnK], ck[MAXM][kGdnK], cv[MAXM][kGdnBV];
   __shared__ float beta_s[MAXM], decay_s[MAXM];
-  __shared__ int par_s[MAXM];
-  __shared__ float2 red[2][4][8], red_n[2][4][8], red_r[4][8];
+  __shared__ int par_s[MAXM], ord_s[MAXM], dep_s[MAXM], br_s[MAXM];
+  __shared__ float2 red[2][4][8], red_n[2][4][8];
   __shared__ int last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hv = blockIdx.x / kGdnNVB, vb = blockIdx.x % kGdnNVB;
@@ -332,6 +380,9 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
       beta_s[tid] = bf16r(1.f / (1.f + expf(-b)));
       decay_s[tid] = expf(a.A[hv] * softplus_f(av + a.dt_bias[hv]));
       par_s[tid] = a.parent && tid > 0 ? tree_parent(a.parent, tid) : tid - 1;
+      ord_s[tid] = a.parent ? a.tinfo[tid] : tid;
+      dep_s[tid] = a.parent ? a.tinfo[32 + tid] : tid;
+      br_s[tid] = a.parent ? a.tinfo[64 + tid] : 0;
     }
   }
   __syncthreads();
@@ -354,6 +405,13 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
     }
     return r;
   };
+  // Nodes in the visiting order (a chain: 0..M-1; a tree: depth first). The state a node starts
+  // from is the previous node's, or -- for a tree node whose parent is not the previous node --
+  // the parent's, kept in a register stack by depth when the parent has several children (a
+  // load of the parent's snapshot would wait for every store still in flight). Parents deeper
+  // than the stack reload their snapshot.
+  constexpr int kStk = TREE ? 8 : 1;
+  float2 stk[kStk][4];
   float2 kv;
   {
     float2 p = make_float2(0.f, 0.f);
@@ -367,56 +425,70 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   }
   float* const obase = a.o_ws + (size_t)hv * kGdnV + v0;
   const size_t head_off = (size_t)hv * kGdnK * kGdnV + v0;
-  for (int t = 0; t < M; ++t) {
-    if (t > 0 && par_s[t] != t - 1) {
-      // Draft tree, a node whose parent is not the previous node: continue from the parent's
-      // snapshot (this lane's own earlier stores) and sum its k_t product afresh. red_r is
-      // written only here; every such exchange is separated from the last by the barrier of a
-      // token exchange, so its reads are done before it is written again.
-      const float* src = a.rec + (size_t)par_s[t] * a.slot_stride + head_off;
-      float2 p = make_float2(0.f, 0.f);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        S[j] = *(const float2*)(src + (size_t)(k0 + j) * kGdnV);
-        const float kk = ck[t][k0 + j];
-        p.x += S[j].x * kk;
-        p.y += S[j].y * kk;
-      }
-      p = make_float2(ksum(p.x), ksum(p.y));
-      if (kg == 0) red_r[wave][vq] = p;
-      __syncthreads();
-      kv = red_r[0][vq];
-#pragma unroll
-      for (int w = 1; w < 4; ++w) {
-        const float2 u = red_r[w][vq];
-        kv.x += u.x;
-        kv.y += u.y;
-      }
-    }
+  for (int i = 0; i < M; ++i) {
+    // wave-uniform values from LDS, kept in scalar registers
+    const int t = TREE ? __builtin_amdgcn_readfirstlane(ord_s[i]) : i;
+    const int tn = i + 1 < M ? (TREE ? __builtin_amdgcn_readfirstlane(ord_s[i + 1]) : i + 1) : t;  // the next node
+    const int pn = TREE && i + 1 < M ? __builtin_amdgcn_readfirstlane(par_s[tn]) : t;  // ... continues from
     const float beta = beta_s[t], eg = decay_s[t];
     const float* vt = &cv[t][c0];
     float2 dv;
     dv.x = beta * (vt[0] - eg * kv.x);
     dv.y = beta * (vt[1] - eg * kv.y);
-    const int tn = min(t + 1, M - 1);  // the next token's k (the last token's sum is unused)
     float2 o = make_float2(0.f, 0.f), nx = o;
     float* dst = a.rec + (size_t)t * a.slot_stride + head_off;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float kk = ck[t][k0 + j], qq = cq[t][k0 + j], kn = ck[tn][k0 + j];
+      const float kk = ck[t][k0 + j], qq = cq[t][k0 + j];
       S[j].x = S[j].x * eg + kk * dv.x;
       S[j].y = S[j].y * eg + kk * dv.y;
       *(float2*)(dst + (size_t)(k0 + j) * kGdnV) = S[j];
       o.x += S[j].x * qq;
       o.y += S[j].y * qq;
-      nx.x += S[j].x * kn;
-      nx.y += S[j].y * kn;
     }
-    // both sums in one exchange: buffer (t + 1) % 2 alternates so the next token's writes never
-    // race this token's reads (the barrier inside wsum separates them)
+    if (TREE && __builtin_amdgcn_readfirstlane(br_s[t])) {  // a branch node, visited again for its later children
+      const int d = __builtin_amdgcn_readfirstlane(dep_s[t]);
+#pragma unroll
+      for (int e = 0; e < kStk; ++e)
+        if (e == d)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) stk[e][j] = S[j];
+    }
+    // the next node's k product from the state it starts from: this node's, or an earlier one's.
+    // The snapshot-load path waits for its loads itself: a load still pending where the paths
+    // meet would make every path wait for the memory counter, i.e. for this node's stores.
+    auto next_sum = [&]() {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float kn = ck[tn][k0 + j];
+        nx.x += S[j].x * kn;
+        nx.y += S[j].y * kn;
+      }
+    };
+    if (!TREE || pn == t) {
+      next_sum();
+    } else {
+      const int d = __builtin_amdgcn_readfirstlane(dep_s[pn]);
+      if (d < kStk) {
+#pragma unroll
+        for (int e = 0; e < kStk; ++e)
+          if (e == d)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) S[j] = stk[e][j];
+        next_sum();
+      } else {
+        const float* src = a.rec + (size_t)pn * a.slot_stride + head_off;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S[j] = *(const float2*)(src + (size_t)(k0 + j) * kGdnV);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) here, so the paths meet with no load pending
+        next_sum();
+      }
+    }
+    // both sums in one exchange: buffer (i + 1) % 2 alternates so the next node's writes never
+    // race this node's reads (the barrier inside wsum separates them)
     o = make_float2(ksum(o.x), ksum(o.y));
     nx = make_float2(ksum(nx.x), ksum(nx.y));
-    const int buf = (t + 1) & 1;
+    const int buf = (i + 1) & 1;
     if (kg == 0) {
       red[buf][wave][vq] = o;
       red_n[buf][wave][vq] = nx;
@@ -488,7 +560,7 @@ extern "C" {
 
 // Workspace: kGdnMaxHV arrival counters (one per 128-byte line) in a fixed region at offset 0,
 // then the head outputs [M, HV V] fp32, normalised q | k [M, 2 H K] fp32, the v conv outputs
-// [M, HV V] bf16 and the gates [M, 2 HV] fp32, each 256-byte aligned. The counters' place does
+// [M, HV V] bf16, the gates [M, 2 HV] fp32 and a tree's visiting order, each 256-byte aligned. The counters' place does
 // not depend on the call's shape, so one zero-filled buffer serves calls of every shape (a
 // shape-dependent layout let one shape's head outputs land on another shape's counters).
 constexpr int kGdnMaxHV = 256;
@@ -498,7 +570,7 @@ size_t tr_gdn_workspace_bytes(int M, int H, int HV) {
   if (M < 1 || M > kGdnMaxTree || H < 1 || HV < 1 || HV > kGdnMaxHV) return 0;
   return gdn_ws_part((size_t)kGdnMaxHV * 32 * sizeof(int)) + gdn_ws_part((size_t)M * HV * kGdnV * sizeof(float)) +
          gdn_ws_part((size_t)M * 2 * H * kGdnK * sizeof(float)) + gdn_ws_part((size_t)M * HV * kGdnV * 2) +
-         gdn_ws_part((size_t)M * 2 * HV * sizeof(float));
+         gdn_ws_part((size_t)M * 2 * HV * sizeof(float)) + gdn_ws_part(3 * 32 * sizeof(int));
 }
 
 }  // extern "C"
@@ -543,6 +615,8 @@ int gdn_launch(const void* qkvz, int ld, const void* x, const void* ba_w, void* 
   a.vconv = (uint16_t*)w;
   w += gdn_ws_part((size_t)M * HV * V * 2);
   a.gates = (float*)w;
+  w += gdn_ws_part((size_t)M * 2 * HV * sizeof(float));
+  a.tinfo = (int*)w;
   a.parent = parent;
   a.node_in = (uint16_t*)node_in;
   a.slot_stride = slot_stride;
@@ -555,15 +629,24 @@ int gdn_launch(const void* qkvz, int ld, const void* x, const void* ba_w, void* 
   a.eps = eps;
   a.scale = 1.f / sqrtf((float)K);
   const int C = 2 * H * K + HV * V;
-  const dim3 prep_grid((C + kGdnThreads - 1) / kGdnThreads + 2 * HV), step_grid(HV * kGdnNVB);
+  // prep: one workgroup per (256 conv channels, group of TG tokens), one per (gate row, group
+  // of 8 tokens), and for a tree one that works out the visiting order
+  const int TG = M <= kGdnMaxM ? gdn_tg<kGdnMaxM>() : gdn_tg<kGdnMaxTree>();
+  const dim3 prep_grid((C + kGdnThreads - 1) / kGdnThreads * ((M + TG - 1) / TG) + 2 * HV * ((M + 7) / 8) +
+                       (parent ? 1 : 0));
+  const dim3 step_grid(HV * kGdnNVB), block(kGdnThreads);
+  hipStream_t st = (hipStream_t)stream;
   if (M <= kGdnMaxM) {
-    hipLaunchKernelGGL(gdn_prep_kernel<kGdnMaxM>, prep_grid, dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(gdn_prep_kernel<kGdnMaxM>, prep_grid, block, 0, st, a);
     if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
-    hipLaunchKernelGGL(gdn_step_kernel<kGdnMaxM>, step_grid, dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+    if (parent)
+      hipLaunchKernelGGL((gdn_step_kernel<kGdnMaxM, true>), step_grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((gdn_step_kernel<kGdnMaxM, false>), step_grid, block, 0, st, a);
   } else {
-    hipLaunchKernelGGL(gdn_prep_kernel<kGdnMaxTree>, prep_grid, dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(gdn_prep_kernel<kGdnMaxTree>, prep_grid, block, 0, st, a);
     if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
-    hipLaunchKernelGGL(gdn_step_kernel<kGdnMaxTree>, step_grid, dim3(kGdnThreads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL((gdn_step_kernel<kGdnMaxTree, true>), step_grid, block, 0, st, a);
   }
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
