@@ -330,7 +330,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer verify-step graph (config 5)")
-    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config4", "config1", "lm_head"],
+    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config4", "config1", "lm_head", "accept"],
                     help="profiling aid: run just this projection's launches (M=8), or the config-5 step graph, and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: run a plain 1 GiB device copy (read 1 GiB, write 1 GiB) and exit")
@@ -351,6 +351,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
+    if a.only == "accept":
+        print(json.dumps({"accept_us": accept_latency(torch, dev)}))
         return
     if a.only == "lm_head":
         print(json.dumps({"lm_head_accept_us_m8": lm_head_accept(torch, dev)}))

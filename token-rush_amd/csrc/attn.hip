@@ -228,6 +228,7 @@ struct AttnSplitArgs {
   float scale;
 };
 
+template <bool TREE>
 __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kAttnBlk * kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[kAttnD * kVPitch];
@@ -235,7 +236,8 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
   const int j = blockIdx.x / a.nsplit, s = blockIdx.x % a.nsplit;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = a.HQ / a.HKV;
-  const int rows = G * a.M - 16 * kAttnWaves * blockIdx.y;  // this workgroup's row group
+  const int gy = TREE ? (int)blockIdx.y : 0;  // row group (a chain's M * G rows fit one)
+  const int rows = G * a.M - 16 * kAttnWaves * gy;  // this workgroup's row group
   const int64_t pos = *a.pos;
   const int64_t L = pos + a.M;
   const int nblk = (int)((L + kAttnBlk - 1) / kAttnBlk);
@@ -246,7 +248,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
   // Q^T operand: lane l holds row 16 wave + l % 16, dims 8 (l / 16) + 32 jj .. + 7
   const int row = 16 * wave + (lane & 15);
   const bool rvalid = row < rows;
-  const int grow = 16 * kAttnWaves * blockIdx.y + row;  // row of the kv head: query qi, head g
+  const int grow = 16 * kAttnWaves * gy + row;  // row of the kv head: query qi, head g
   const int qi = rvalid ? grow / G : 0;
   const int hq = j * G + (rvalid ? grow % G : 0);
   uint4 qb[8];
@@ -257,7 +259,8 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
   // The new keys query qi sees: rows pos + i for the bits i of vis -- i <= qi for a chain, the
   // node's ancestors and itself for a tree.
   uint32_t vis = qi >= 31 ? ~0u : (2u << qi) - 1u;
-  if (a.parent) {
+  const int64_t qlimit = pos + qi;  // a chain's last visible row
+  if (TREE) {
     vis = 0;
     int jn = qi;
     for (int d = 0; d < kAttnMaxTree; ++d) {
@@ -359,12 +362,18 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
     // mask, online softmax (this lane: one row, 8 keys)
     float sc[8];
     float mx = -INFINITY;
+    // a block of committed rows only (all before pos) needs no mask; in the others key rel =
+    // kidx - pos < M selects a bit of vis when >= 0
+    const bool committed = TREE && key0 + kAttnBlk <= pos;  // uniform
+    const int rel0 = TREE ? (int)(key0 - pos) + 4 * (lane >> 4) : 0;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t kidx = key0 + 16 * kt + 4 * (lane >> 4) + r;
-        const bool allowed = rvalid && kidx < L && (kidx < pos || ((vis >> (int)(kidx - pos)) & 1u));
+        const int rel = rel0 + 16 * kt + r;
+        const bool allowed =
+            TREE ? rvalid && (committed || (rel < a.M && (rel < 0 || ((vis >> rel) & 1u))))
+                 : rvalid && key0 + 16 * kt + 4 * (lane >> 4) + r < L && key0 + 16 * kt + 4 * (lane >> 4) + r <= qlimit;
         const float v = allowed ? st[kt][r] * a.scale : -INFINITY;
         sc[4 * kt + r] = v;
         mx = fmaxf(mx, v);
@@ -549,7 +558,12 @@ int attn_decode_launch(const void* q, const void* qkv, int ld, const void* k_cac
   s.scale = 1.f / sqrtf((float)D);
   // the G M query rows of a kv head in groups of 64 (one 16-row tile per wave)
   const int groups = ((HQ / HKV) * M + 16 * kAttnWaves - 1) / (16 * kAttnWaves);
-  hipLaunchKernelGGL(attn_split_kernel, dim3(HKV * nsplit, groups), dim3(64 * kAttnWaves), 0, (hipStream_t)stream, s);
+  if (parent)
+    hipLaunchKernelGGL(attn_split_kernel<true>, dim3(HKV * nsplit, groups), dim3(64 * kAttnWaves), 0,
+                       (hipStream_t)stream, s);
+  else
+    hipLaunchKernelGGL(attn_split_kernel<false>, dim3(HKV * nsplit, groups), dim3(64 * kAttnWaves), 0,
+                       (hipStream_t)stream, s);
   if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
   AttnReduceArgs r;
   r.m_part = s.m_part;
@@ -581,7 +595,8 @@ int tr_attn_decode(const void* q, const void* qkv, int ld, const void* k_cache, 
                    const float* k_scale, const float* v_scale, int maxlen, const int64_t* pos, void* out,
                    void* workspace, size_t workspace_bytes, int M, int HQ, int HKV, int D, int nsplit, void* stream) {
   if (M == 0) return TR_OK;
-  if (M < 0 || M > kAttnMaxM) return TR_ERR_SHAPE;
+  // a chain's query rows of one kv head fit one workgroup's four 16-row tiles
+  if (M < 0 || M > kAttnMaxM || HQ < 1 || HKV < 1 || (HQ / HKV) * M > 16 * kAttnWaves) return TR_ERR_SHAPE;
   return attn_decode_launch(q, qkv, ld, k_cache, v_cache, k_scale, v_scale, maxlen, pos, out, workspace,
                             workspace_bytes, M, HQ, HKV, D, nsplit, nullptr, stream);
 }

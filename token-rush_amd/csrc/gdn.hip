@@ -142,7 +142,7 @@ __device__ void tree_order(const int32_t* parent, int M, int* info) {
 
 // ------------------------------------------------------------------ prep: conv, norms, gates
 
-template <int MAXM>
+template <int MAXM, bool TREE>
 __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
   constexpr int TG = gdn_tg<MAXM>();
   __shared__ float part[4][8];
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
   const int C = 2 * QK + a.HV * kGdnV;
   const int n_cb = (C + kGdnThreads - 1) / kGdnThreads;
   const int n_conv = n_cb * ((M + TG - 1) / TG);
-  if (a.parent && blockIdx.x == gridDim.x - 1) {
+  if (TREE && blockIdx.x == gridDim.x - 1) {
     tree_order(a.parent, M, a.tinfo);
     return;
   }
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
     const int ch = cb * kGdnThreads + tid;
     const bool on = ch < C;
     const int pr = (int)(*a.pos % a.R);  // ring column of token 0
-    if (a.parent && tid < M) {
+    if (TREE && tid < M) {
       int j = tid, dep = 0;
       for (int s = 0; s < MAXM && j > 0; ++s) {
         j = tree_parent(a.parent, j);
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
         }
       }
     }
-    if (a.parent) __syncthreads();
+    if (TREE) __syncthreads();
     float y[TG];
 #pragma unroll
     for (int u = 0; u < TG; ++u) y[u] = 0.f;
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
         const int t = min(t0 + u, M - 1);
         xin[u] = a.qkvz[(size_t)t * a.ld + ch];
         win[u + 3] = bf16_bits_to_f32(t0 + u < M ? xin[u] : (uint16_t)0);
-        if (a.parent)
+        if (TREE)
 #pragma unroll
           for (int k = 0; k < 3; ++k) {
             const int sn = src_s[t][k];
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
           // oldest first: 3 back, 2 back, 1 back, the token itself (a chain's group starts at
           // token 0, so its window is win[u .. u + 3])
           float sv[3] = {win[u + 2], win[u + 1], win[u]};
-          if (a.parent)
+          if (TREE)
 #pragma unroll
             for (int k = 0; k < 3; ++k) {
               const int sn = src_s[t][k];
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
           y[u] = bf16r(yv / (1.f + expf(-yv)));
         }
       }
-      if (a.parent) {  // a tree's inputs wait for the commit
+      if (TREE) {  // a tree's inputs wait for the commit
 #pragma unroll
         for (int u = 0; u < TG; ++u)
           if (t0 + u < M) a.node_in[(size_t)(t0 + u) * C + ch] = xin[u];
@@ -379,10 +379,10 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
     if (tid < M) {
       beta_s[tid] = bf16r(1.f / (1.f + expf(-b)));
       decay_s[tid] = expf(a.A[hv] * softplus_f(av + a.dt_bias[hv]));
-      par_s[tid] = a.parent && tid > 0 ? tree_parent(a.parent, tid) : tid - 1;
-      ord_s[tid] = a.parent ? a.tinfo[tid] : tid;
-      dep_s[tid] = a.parent ? a.tinfo[32 + tid] : tid;
-      br_s[tid] = a.parent ? a.tinfo[64 + tid] : 0;
+      par_s[tid] = TREE && tid > 0 ? tree_parent(a.parent, tid) : tid - 1;
+      ord_s[tid] = TREE ? a.tinfo[tid] : tid;
+      dep_s[tid] = TREE ? a.tinfo[32 + tid] : tid;
+      br_s[tid] = TREE ? a.tinfo[64 + tid] : 0;
     }
   }
   __syncthreads();
@@ -636,15 +636,16 @@ int gdn_launch(const void* qkvz, int ld, const void* x, const void* ba_w, void* 
                        (parent ? 1 : 0));
   const dim3 step_grid(HV * kGdnNVB), block(kGdnThreads);
   hipStream_t st = (hipStream_t)stream;
-  if (M <= kGdnMaxM) {
-    hipLaunchKernelGGL(gdn_prep_kernel<kGdnMaxM>, prep_grid, block, 0, st, a);
+  if (M <= kGdnMaxM && !parent) {
+    hipLaunchKernelGGL((gdn_prep_kernel<kGdnMaxM, false>), prep_grid, block, 0, st, a);
     if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
-    if (parent)
-      hipLaunchKernelGGL((gdn_step_kernel<kGdnMaxM, true>), step_grid, block, 0, st, a);
-    else
-      hipLaunchKernelGGL((gdn_step_kernel<kGdnMaxM, false>), step_grid, block, 0, st, a);
+    hipLaunchKernelGGL((gdn_step_kernel<kGdnMaxM, false>), step_grid, block, 0, st, a);
+  } else if (M <= kGdnMaxM) {
+    hipLaunchKernelGGL((gdn_prep_kernel<kGdnMaxM, true>), prep_grid, block, 0, st, a);
+    if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
+    hipLaunchKernelGGL((gdn_step_kernel<kGdnMaxM, true>), step_grid, block, 0, st, a);
   } else {
-    hipLaunchKernelGGL(gdn_prep_kernel<kGdnMaxTree>, prep_grid, block, 0, st, a);
+    hipLaunchKernelGGL((gdn_prep_kernel<kGdnMaxTree, true>), prep_grid, block, 0, st, a);
     if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
     hipLaunchKernelGGL((gdn_step_kernel<kGdnMaxTree, true>), step_grid, block, 0, st, a);
   }

@@ -11,7 +11,8 @@ import os
 import torch  # loads torch's HIP runtime first; the library binds to the same libamdhip64.so.7
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libtrhip.so")
+# TOKENRUSH_HIP_LIB names another build of the same library (e.g. an instrumented one)
+LIB_PATH = os.environ.get("TOKENRUSH_HIP_LIB") or os.path.join(_HERE, "libtrhip.so")
 
 # Error codes (tr_common.h). 1 and 2 mean what the reference's Marlin launcher means by
 # them (marlin_bf16.cu:627-669, marlin_bf16.cpp:41-43).
