@@ -281,6 +281,119 @@ __device__ void select_top64(const uint32_t (&k16)[E], const uint32_t (&idx)[E],
 }
 
 
+// Helpers of the threshold top-64 (sample_kernel). Every item's key is unique (value, then index),
+// so ranks and the resulting list do not depend on the order candidates were gathered in.
+
+// The largest v with at least K of the wave's 64 * R keys >= v (bit by bit from the top):
+// uniform over the wave.
+template <int K, int R>
+__device__ __forceinline__ uint32_t wave_kth(const uint32_t (&kv)[R]) {
+  uint32_t v = 0;
+#pragma unroll
+  for (int b = 15; b >= 0; --b) {
+    const uint32_t c = v | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) cnt += __popcll(__ballot(kv[r] >= c));
+    v = cnt >= K ? c : v;
+  }
+  return v;
+}
+
+// The top 64 of n <= kTopCap candidate keys (vkey()s) in LDS, by rank: thread t compares
+// candidate t % kTopCap with one half of the others, the halves' counts meet in rank[] (zeroed
+// by the caller), and the candidates of rank < 64 land at their rank. 256 threads.
+constexpr int kTopCap = 128;
+__device__ void lds_rank_top64(const uint64_t* kk, int n, int* rank, uint32_t* out_k, uint32_t* out_i) {
+  const int tid = threadIdx.x, c = tid & (kTopCap - 1), half = tid >> 7;
+  if (c < n) {
+    const uint64_t key = kk[c];
+    int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+    const int j0 = half * (kTopCap / 2);
+#pragma unroll
+    for (int j = 0; j < kTopCap / 2; j += 4) {  // slots past n hold 0: below every key
+      r0 += kk[j0 + j] > key;
+      r1 += kk[j0 + j + 1] > key;
+      r2 += kk[j0 + j + 2] > key;
+      r3 += kk[j0 + j + 3] > key;
+    }
+    atomicAdd(&rank[c], (r0 + r1) + (r2 + r3));
+  }
+  __syncthreads();
+  if (tid < n) {
+    const int r = rank[tid];
+    if (r < kCand) {
+      out_k[r] = (uint32_t)(kk[tid] >> 32);
+      out_i[r] = vkey_idx(kk[tid]);
+    }
+  }
+  __syncthreads();
+}
+
+// Appends this thread's items with keys >= tau (flags[e]) to kk[] as vkey()s: positions from
+// per-item ballots within the wave, one LDS atomic per wave for the wave's base. Returns the
+// total after a barrier (uniform); nothing is written when it exceeds kTopCap.
+template <int E>
+__device__ int lds_append_keys(const uint32_t (&k16)[E], const uint32_t (&idx)[E], uint32_t tau, uint64_t* kk, int* cnt) {
+  const int lane = threadIdx.x & 63;
+  int wtot = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) wtot += __popcll(__ballot(k16[e] >= tau));
+  int base = 0;
+  if (lane == 0 && wtot) base = atomicAdd(cnt, wtot);
+  base = __shfl(base, 0);
+  __syncthreads();
+  const int tot = *cnt;
+  if (tot <= kTopCap) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const unsigned long long m = __ballot(k16[e] >= tau);
+      if (k16[e] >= tau) kk[base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] =
+          vkey(k16[e], idx[e]);
+      base += __popcll(m);
+    }
+  }
+  __syncthreads();
+  return tot;
+}
+
+// Top-64 of a chunk by a threshold (the fast path of sample_kernel's per-chunk select). tau =
+// the 64th largest of the 256 thread maxima bounds the chunk's 64th largest key from below: the
+// 64 threads whose maxima reach it hold 64 items >= tau. Items >= tau (typically ~75 of 4096 for
+// continuous data) are ranked; more than kTopCap of them (heavy ties, padding) take select_top64
+// instead. Both give the same list: the exact top 64, value descending then index ascending.
+template <int E>
+__device__ void select_top64_thr(const uint32_t (&k16)[E], const uint32_t (&idx)[E], uint32_t* out_k, uint32_t* out_i) {
+  __shared__ uint64_t kk[kTopCap];
+  __shared__ int rank[kTopCap];
+  __shared__ uint32_t tmax[256];
+  __shared__ uint32_t s_tau;
+  __shared__ int s_cnt;
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t m = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) m = k16[e] > m ? k16[e] : m;
+  tmax[tid] = m;
+  if (tid < kTopCap) {
+    kk[tid] = 0ull;
+    rank[tid] = 0;
+  }
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  if (tid < 64) {
+    const uint32_t mv[4] = {tmax[lane], tmax[64 + lane], tmax[128 + lane], tmax[192 + lane]};
+    const uint32_t v = wave_kth<kCand>(mv);
+    if (lane == 0) s_tau = v;
+  }
+  __syncthreads();
+  const int tot = lds_append_keys(k16, idx, s_tau, kk, &s_cnt);
+  if (tot > kTopCap) {  // uniform
+    select_top64<E>(k16, idx, out_k, out_i);
+    return;
+  }
+  lds_rank_top64(kk, tot, rank, out_k, out_i);
+}
+
 // Wave-wide merge of two descending 64-key lists, one key per lane: lane i keeps the larger of
 // a[i] and b[63 - i] (the top 64 of the union, as a bitonic sequence), then a bitonic merge
 // sorts it descending. Keys are vkey()s: value descending, index ascending.
@@ -336,6 +449,45 @@ __device__ void merge_lists_top64(const uint32_t* src, int n, uint32_t* out_k, u
     out_i[lane] = vkey_idx(acc);
   }
   __syncthreads();
+}
+
+// The row's top 64 from n <= 64 sorted chunk lists (as merge_lists_top64), by a threshold: tau =
+// the 64th largest of the lists' first four keys bounds the row's 64th largest from below; the
+// entries >= tau (a prefix of each list, typically ~70 in all) are ranked as in
+// select_top64_thr. More than kTopCap of them take merge_lists_top64 instead; both give the same
+// list. Wave w loads ranks 16 w .. 16 w + 15 of list `lane`, all loads issued at once.
+__device__ void merge_lists_top64_thr(const uint32_t* src, int n, uint32_t* out_k, uint32_t* out_i) {
+  constexpr int kR = 16;
+  __shared__ uint64_t kk[kTopCap];
+  __shared__ int rank[kTopCap];
+  __shared__ uint32_t s_tau;
+  __shared__ int s_cnt;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = lane < n ? lane : n - 1;
+  uint32_t kv[kR], iv[kR];
+#pragma unroll
+  for (int j = 0; j < kR; ++j) {
+    const uint64_t v = ws_ld((const uint64_t*)(src + (size_t)c * kCand * 2 + 2 * (kR * wid + j)));
+    kv[j] = lane < n ? (uint32_t)v : 0u;
+    iv[j] = (uint32_t)(v >> 32);
+  }
+  if (tid < kTopCap) {
+    kk[tid] = 0ull;
+    rank[tid] = 0;
+  }
+  if (tid == 0) s_cnt = 0;
+  if (wid == 0) {
+    const uint32_t head[4] = {kv[0], kv[1], kv[2], kv[3]};
+    const uint32_t v = wave_kth<kCand>(head);
+    if (lane == 0) s_tau = v;
+  }
+  __syncthreads();
+  const int tot = lds_append_keys(kv, iv, s_tau, kk, &s_cnt);
+  if (tot > kTopCap) {  // uniform
+    merge_lists_top64(src, n, out_k, out_i);
+    return;
+  }
+  lds_rank_top64(kk, tot, rank, out_k, out_i);
 }
 
 // ------------------------------------------------------------------ accept outputs
@@ -499,14 +651,14 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
       k16[e] = i < a.V ? ord16(lg[i]) : 0u;
     }
   }
-  select_top64<E>(k16, idx, tk, ti);
+  select_top64_thr<E>(k16, idx, tk, ti);
   uint32_t* mine = a.cand + ((size_t)row * a.nch + ch) * kCand * 2;
   if (threadIdx.x < kCand) {
     ws_st(mine + 2 * threadIdx.x, tk[threadIdx.x]);
     ws_st(mine + 2 * threadIdx.x + 1, ti[threadIdx.x]);
   }
   if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
-  merge_lists_top64(a.cand + (size_t)row * a.nch * kCand * 2, a.nch, tk, ti);
+  merge_lists_top64_thr(a.cand + (size_t)row * a.nch * kCand * 2, a.nch, tk, ti);
   if (threadIdx.x < 64) {
     const int64_t t = sample_pick(tk, ti, *a.temperature, *a.top_p, *a.top_k, a.u[row]);
     if (threadIdx.x == 0) {
