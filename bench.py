@@ -291,6 +291,58 @@ def config4_tree_step(torch, dev, model, reps=10, M=32):
                     "accept, commit of KV rows/scales (4 launches) and conv rings (1 launch)"}
 
 
+TL_MARKS = {0: "entry", 1: "launch constants", 3: "first two strips issued", 2: "activations staged",
+            4: "prologue end", 5: "strip 0 MACs", 6: "strip 1 MACs", 7: "strip 2 MACs", 8: "strip 3 MACs",
+            9: "strip 4 MACs", 10: "strip 5 MACs", 16: "batch reduced (last)", 20: "strip loop exit"}
+
+
+def gemm_timeline(torch, gfx950, dev, name, M=M_VERIFY, launches=6):
+    """The in-kernel timeline of one projection's GEMM (a -DTR_TIMELINE build of the library,
+    named by TOKENRUSH_HIP_LIB): s_memrealtime stamps per wave at fixed points, one launch at a time
+    on weights not read before (HBM, not cache). Returns per-mark percentiles (0, 10, 50, 90, 100)
+    over the launch's waves, in us from the launch's first wave entry."""
+    import ctypes
+    import numpy as np
+    from tokenrush_amd import _lib
+    lib = _lib.lib()
+    if not hasattr(lib, "tr_gemm_timeline"):
+        raise SystemExit("--timeline needs TOKENRUSH_HIP_LIB=token-rush_amd/tokenrush_amd/libtrhip_timeline.so "
+                         "(make -C token-rush_amd/csrc timeline)")
+    lib.tr_gemm_timeline.restype = ctypes.c_void_p
+    lib.tr_gemm_timeline.argtypes = [ctypes.POINTER(ctypes.c_size_t)]
+    nbytes = ctypes.c_size_t(0)
+    buf = lib.tr_gemm_timeline(ctypes.byref(nbytes))
+    hip = ctypes.CDLL("libamdhip64.so")
+    j = [n for n, _, _, _ in LAYER_SET].index(name)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+    copies = [make_layer_set(torch, gfx950, gen, dev)[j] for _ in range(launches + 1)]
+    x = torch.randn(M, LAYER_SET[j][2], device=dev, generator=gen).to(torch.bfloat16)
+    call(gfx950, x, copies[-1])                      # first call: workspaces, code load
+    torch.cuda.synchronize()
+    host = np.zeros(nbytes.value // 8, dtype=np.uint64)
+    stamps = {k: [] for k in TL_MARKS}
+    spans = []
+    for c in copies[:launches]:
+        hip.hipMemset(ctypes.c_void_p(buf), 0, ctypes.c_size_t(nbytes.value))
+        hip.hipDeviceSynchronize()
+        call(gfx950, x, c)
+        torch.cuda.synchronize()
+        hip.hipMemcpy(ctypes.c_void_p(host.ctypes.data), ctypes.c_void_p(buf), ctypes.c_size_t(nbytes.value), 2)
+        t = host.reshape(-1, 16, 24).astype(np.int64)
+        live = t[:, :, 0] > 0
+        t0 = t[:, :, 0][live].min()
+        for k in TL_MARKS:
+            v = t[:, :, k][live & (t[:, :, k] > 0)]
+            stamps[k].extend(((v - t0) / 100.0).tolist())
+        spans.append((t[:, :, 20][live].max() - t0) / 100.0)
+    pct = {TL_MARKS[k]: [round(float(q), 2) for q in np.percentile(v, [0, 10, 50, 90, 100])]
+           for k, v in stamps.items() if v}
+    return {"timeline": name, "M": M, "launches": launches, "workgroups_x_waves": int(len(stamps[0]) / launches),
+            "us_from_first_entry_p0_p10_p50_p90_p100": pct, "last_wave_exit_us": [round(s_, 2) for s_ in spans],
+            "note": "one launch at a time on weights not read before; stamps by lane 0 of each wave (100 MHz)"}
+
+
 def cpu_baseline(M=M_VERIFY, min_reps=5, budget_s=10.0):
     """The reference's CPU path restated (oracle.int4.torch_dequant_linear: torch unpack, in-place
     fp16 dequant, F.linear in bf16) over one layer set at M rows on the host's CPU share; median of
@@ -332,6 +384,9 @@ def main():
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer verify-step graph (config 5)")
     ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config4", "config1", "lm_head", "accept"],
                     help="profiling aid: run just this projection's launches (M=8), or the config-5 step graph, and exit")
+    ap.add_argument("--timeline", choices=[n for n, _, _, _ in LAYER_SET],
+                    help="profiling aid: the in-kernel timeline of this projection's GEMM at M=8 (needs the "
+                         "TR_TIMELINE build named by TOKENRUSH_HIP_LIB)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: run a plain 1 GiB device copy (read 1 GiB, write 1 GiB) and exit")
     a = ap.parse_args()
@@ -351,6 +406,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
+    if a.timeline:
+        print(json.dumps(gemm_timeline(torch, gfx950, dev, a.timeline)))
         return
     if a.only == "accept":
         print(json.dumps({"accept_us": accept_latency(torch, dev)}))

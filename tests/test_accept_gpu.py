@@ -88,6 +88,25 @@ def test_sample_config3_rows(dev, T, top_p, top_k):
         assert np.array_equal(got, oa.sample(lg, T, top_p, top_k, u)), trial
 
 
+def test_sample_heavy_ties_full_vocab(dev):
+    """Integer-valued logits at V = 248320: thousands of equal values around every chunk's and
+    row's 64th largest, so the threshold selects overflow and both exact fallbacks (the radix
+    select per chunk, the bitonic list merge per row) run; a second set mixes a tied row with
+    continuous ones."""
+    from tokenrush_amd.sample import SamplingParams, sample
+    say("sample heavy ties")
+    rng = np.random.default_rng(31)
+    lg = np.round(rng.standard_normal((8, V_FULL))).astype(F)
+    lg[4:] = oa.planted_logits(4, V_FULL, seed=32)
+    x = dev_logits(lg)
+    p = SamplingParams(dev)
+    for T, top_p, top_k in ((1.0, 1.0, 64), (0.8, 0.9, 50), (0.0, 1.0, 64)):
+        p.set(temperature=T, top_p=top_p, top_k=top_k)
+        u = rng.random(8).astype(F)
+        got = sample(x, p, torch.from_numpy(u).to(dev)).cpu().numpy()
+        assert np.array_equal(got, oa.sample(lg, T, top_p, top_k, u)), (T, top_p, top_k)
+
+
 def test_sample_small_and_peaked(dev):
     """The reference's test_sample.py:75-88 rows plus a vocabulary smaller than a chunk."""
     from tokenrush_amd.sample import SamplingParams, sample

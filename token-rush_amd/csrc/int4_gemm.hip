@@ -47,6 +47,26 @@
 
 namespace tr {
 
+// In-kernel timeline (a build with -DTR_TIMELINE only, `make timeline`): wave w of workgroup b
+// writes s_memrealtime (100 MHz) at mark i to tr_tl_buf[(b * 16 + w) * kTlMarks + i]. Marks: 0
+// entry, 1 launch constants ready, 2 activations staged, 3 the first two strips issued, 4
+// prologue end (group sums), 5 + r strip r's MACs done (r < 11), 16 a batch's reduction done,
+// 20 exit of the strip loop. The normal build has none of it.
+#ifdef TR_TIMELINE
+constexpr int kTlMarks = 24, kTlBlocks = 2048;
+__device__ unsigned long long tr_tl_buf[kTlBlocks * 16 * kTlMarks];
+#define TLM(i)                                                                                       \
+  do {                                                                                               \
+    const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                                  \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < kTlBlocks)                                           \
+      tr_tl_buf[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * kTlMarks + (i)] = t_;               \
+  } while (0)
+#else
+#define TLM(i) \
+  do {         \
+  } while (0)
+#endif
+
 constexpr int kGroup = 128;
 constexpr int kQuad = 4;                          // groups per quad
 constexpr int kCodeBytes = 1024;                  // one group's codes for 16 rows
@@ -220,6 +240,7 @@ __device__ __forceinline__ int udiv_small(uint32_t q, int d, uint32_t magic) {
 template <int MT, int GW, bool F16S, bool XDMA>
 __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   extern __shared__ float red[];  // [2][RB][W][MT][64][4]
+  TLM(0);
   __shared__ uint64_t rowbest[32];  // fused argmax: best key per output row
   if (threadIdx.x < 32) rowbest[threadIdx.x] = 0;
   const int G = a.K / kGroup;
@@ -253,6 +274,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   const int oob = a.wbytes;
   auto strip_off = [&](int r) { return __builtin_amdgcn_readfirstlane(r < r1 ? phys(r) * quad_stride + blk_off : oob); };
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.packed, (short)0, oob, 0x00020000);
+  TLM(1);
   const int lane_off = 16 * lane;
   // parameters of row lane % 16, groups gbase % 4 .. + GW - 1, relative to the strip offset
   const int sm_voff = kSmOff + 16 * (lane & 15) + 4 * (gbase % kQuad) - (gbase % kQuad) * kCodeBytes;
@@ -306,8 +328,10 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   if constexpr (XDMA) __builtin_amdgcn_s_barrier();
   load_strip<GW>(buf[0], rsrc, active ? strip_off(r0) : oob, lane_off, sm_voff);
   load_strip<GW>(buf[1], rsrc, active ? strip_off(r0 + 1) : oob, lane_off, sm_voff);
+  TLM(3);
   if constexpr (XDMA) {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (GW + 1)) : "memory");  // the staging loads have landed
+    TLM(2);
     const char* stage = (const char*)red + a.xstage_off + wave * (GW * 2048);
     const int i = lane & 15;
 #pragma unroll
@@ -347,6 +371,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
       Xa[mt] = xs;
     }
   }
+  TLM(4);
   const int slot16 = lane >> 4;
   const StripWalk walk16(threadIdx.x, 4, blockDim.x, a.M, a.magicM), walk8(threadIdx.x, 3, blockDim.x, a.M, a.magicM);
 
@@ -367,6 +392,12 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
         for (int gw = 0; gw < GW; ++gw) tile_mac<MT, F16S>(buf[h].w[gw], buf[h].sm[gw], xa[gw], acc, kExp128);
         min_fold<MT, GW, F16S>(buf[h].sm, Xa, slot16, acc);
       }
+#ifdef TR_TIMELINE
+      if (r < 11) {
+        asm volatile("" ::"v"(acc[0][0]), "v"(acc[0][3]));  // the strip's MACs before the stamp
+        TLM(5 + r);
+      }
+#endif
       // The refill is issued on every path (out-of-range offsets for inactive waves and past the
       // range: zeros, no memory access), so every path has the same loads in flight and the
       // compiler's wait before the next strip's compute covers that strip's loads only -- a
@@ -425,6 +456,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
           }
           sib = 0;
           half ^= 1;
+          TLM(16);
         } else {
           ++sib;
         }
@@ -466,6 +498,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     if (a.spec && threadIdx.x < 64) finish_chain(pred, spec, a.M, a.o);
     return;
   }
+  TLM(20);
   if (a.mode != OUT_BF16_VIA_WS) return;
   // Last-arriving slot of this row range sums the S partials in slot order -> bf16. The
   // partials were stored at agent scope; waiting for those stores to complete before the
@@ -1011,5 +1044,15 @@ int tr_dequant_int4(const void* qweight, const void* scale, const void* mn, void
     return TR_ERR_ARG;
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
+
+#ifdef TR_TIMELINE
+// The timeline buffer of a -DTR_TIMELINE build (device address, size in bytes).
+void* tr_gemm_timeline(size_t* bytes) {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(tr_tl_buf)) != hipSuccess) return nullptr;
+  if (bytes) *bytes = sizeof(tr_tl_buf);
+  return p;
+}
+#endif
 
 }  // extern "C"
