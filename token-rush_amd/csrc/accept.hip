@@ -68,35 +68,31 @@ __device__ __forceinline__ float wave_seq_sum(const float (&r)[R]) {
   return s;
 }
 // Running sums acc + x_0 + ... + x_j (left to right): lane i of pre[k] gets element 64 k + i's.
-// Every lane runs the same chain and stores each sum to the wave's LDS scratch (64 R floats; all
-// lanes write the same value to the same word), then reads back its own. The chain is not put
-// under a lane-0 branch: the compiler would sink the computation of the values that v_readlane
-// reads into that branch, leaving the other lanes' values uncomputed.
+// The chain is the one above; each sum is placed into its lane with v_writelane (a store of the
+// same word by all 64 lanes at every step, then a read back, took twice the chain's time).
 template <int R>
-__device__ __forceinline__ void wave_seq_prefix(const float (&r)[R], float acc, float (&pre)[R], float* lds) {
-  const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void wave_seq_prefix(const float (&r)[R], float acc, float (&pre)[R]) {
 #pragma unroll
   for (int k = 0; k < R; ++k) {
     float x = r[k];
+    int p = 0;
+    const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < 64; ++i) {
-      if ((i & 15) == 0) asm volatile("" : "+v"(x), "+v"(acc));
+      if ((i & 15) == 0) asm volatile("" : "+v"(x), "+v"(acc), "+v"(p));
       acc = __fadd_rn(acc, lane_val(x, i));
-      lds[64 * k + i] = acc;
+      p = lane == i ? __float_as_int(acc) : p;
     }
+    pre[k] = __int_as_float(p);
   }
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int k = 0; k < R; ++k) pre[k] = lds[64 * k + lane];
-  __builtin_amdgcn_wave_barrier();
 }
 // The sequential inverse-CDF step: the first element whose running sum exceeds target, else the
 // last positive element (-1 if none); *base gets the running sum before it. Uniform result.
 // lds: 64 R floats of scratch.
+// Given the running sums pre of r from acc: the first element whose running sum exceeds target,
+// else the last positive element (-1 if none); *base gets the running sum before it. Uniform.
 template <int R>
-__device__ __forceinline__ int wave_seq_search(const float (&r)[R], float acc, float target, float* base, float* lds) {
-  float pre[R];
-  wave_seq_prefix(r, acc, pre, lds);
+__device__ __forceinline__ int wave_seq_choose(const float (&r)[R], const float (&pre)[R], float acc, float target, float* base) {
   int chosen = -1;
 #pragma unroll
   for (int k = 0; k < R; ++k) {
@@ -119,6 +115,13 @@ __device__ __forceinline__ int wave_seq_search(const float (&r)[R], float acc, f
   }
   *base = b;
   return chosen;
+}
+// The sequential inverse-CDF step over r from acc (wave_seq_choose of wave_seq_prefix).
+template <int R>
+__device__ __forceinline__ int wave_seq_search(const float (&r)[R], float acc, float target, float* base) {
+  float pre[R];
+  wave_seq_prefix(r, acc, pre);
+  return wave_seq_choose(r, pre, acc, target, base);
 }
 
 // Block-wide exclusive prefix sum of one int per thread (blockDim.x <= 1024), plus the total.
@@ -608,14 +611,13 @@ __device__ int64_t sample_pick(const uint32_t* tk, const uint32_t* ti, float T, 
   const float er[1] = {e};
   const float p = __fdiv_rn(e, wave_seq_sum(er));
   // cumulative sums in rank order; lane i keeps the sum through rank i
-  __shared__ float cum_s[kCand];
   const float pr[1] = {p};
   float cum[1];
-  wave_seq_prefix(pr, 0.f, cum, cum_s);
+  wave_seq_prefix(pr, 0.f, cum);
   const bool keep = __fsub_rn(cum[0], p) < top_p && i < top_k;
   const float pk[1] = {keep ? p : 0.f};
   float cum2[1];
-  wave_seq_prefix(pk, 0.f, cum2, cum_s);
+  wave_seq_prefix(pk, 0.f, cum2);
   const float target = __fmul_rn(u, lane_val(cum2[0], kCand - 1));
   const float mycum2 = cum2[0];
   const unsigned long long below = __ballot(mycum2 < target);
@@ -689,28 +691,33 @@ struct ResidualArgs {
   float* chunk_sum;        // ws [M * nch] (phase 2), then [nch] (phase 3)
   float* Z;                // ws [M]
   float* e_draft;          // ws [M]
+  float* q_draft;          // ws [M]: q_i(d_i), stored by the workgroup whose chunk holds d_i
   int* n_ws;               // ws [1]: accepted drafts, read by phase 3
   int* cnt_rows;
   int* cnt_all;
   AcceptOut o;
 };
 
-// This lane's run (16 elements) of r for chunk ch of row `row`: r = e / Z - q clamped at 0
-// (residual), or e / Z (bonus), or e (phase 2, Z unused). Returns the sequential run sum.
+// This lane's run (16 elements) of chunk ch of row `row`: logits bits as loaded (two per word,
+// unpacked only where used, so that a load can stay in flight), and q (residual only).
+struct RunData {
+  uint32_t lw[kRun / 2];
+  float qv[kRun];
+};
 template <int MODE>  // 0: e, 1: residual, 2: p
-__device__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float Zr, float (&vals)[kRun]) {
+__device__ __forceinline__ void run_load(const ResidualArgs& a, int row, int ch, int lane, RunData& d) {
   const uint16_t* lg = a.logits + (size_t)row * a.V;
   const float* qr = a.q + (size_t)row * a.V;
   const int i0 = ch * kChunk + lane * kRun;
-  uint32_t lb[kRun];
-  float qv[kRun];
+  float (&qv)[kRun] = d.qv;
   if ((a.V & 7) == 0 && i0 + kRun <= a.V) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint4 v = *(const uint4*)(lg + i0 + 8 * h);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lb[8 * h + e] = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      d.lw[4 * h] = v.x;
+      d.lw[4 * h + 1] = v.y;
+      d.lw[4 * h + 2] = v.z;
+      d.lw[4 * h + 3] = v.w;
     }
     if (MODE == 1) {
 #pragma unroll
@@ -725,16 +732,24 @@ __device__ float run_values(const ResidualArgs& a, int row, int ch, int lane, fl
   } else {
 #pragma unroll
     for (int e = 0; e < kRun; ++e) {
-      lb[e] = i0 + e < a.V ? lg[i0 + e] : 0u;
+      const uint32_t b = i0 + e < a.V ? lg[i0 + e] : 0u;
+      d.lw[e >> 1] = (e & 1) ? (d.lw[e >> 1] | (b << 16)) : b;
       if (MODE == 1) qv[e] = i0 + e < a.V ? qr[i0 + e] : 0.f;
     }
   }
+}
+// The run's values of r from its loaded data: r = e / Z - q clamped at 0 (residual), or e / Z
+// (bonus), or e (phase 2, Z unused). Returns the sequential run sum.
+template <int MODE>
+__device__ __forceinline__ float run_finish(const ResidualArgs& a, int ch, int lane, float mx, float Zr, const RunData& d, float (&vals)[kRun]) {
+  const int i0 = ch * kChunk + lane * kRun;
+  const float (&qv)[kRun] = d.qv;
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < kRun; ++e) {
     float v = 0.f;
     if (i0 + e < a.V) {
-      v = texp(__fsub_rn(bf16_bits_to_f32(lb[e]), mx));
+      v = texp(__fsub_rn(bf16_bits_to_f32((d.lw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), mx));
       if (MODE >= 1) v = __fdiv_rn(v, Zr);
       if (MODE == 1) {
         v = __fsub_rn(v, qv[e]);
@@ -745,6 +760,12 @@ __device__ float run_values(const ResidualArgs& a, int row, int ch, int lane, fl
     s = __fadd_rn(s, v);
   }
   return s;
+}
+template <int MODE>
+__device__ __forceinline__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float Zr, float (&vals)[kRun]) {
+  RunData d;
+  run_load<MODE>(a, row, ch, lane, d);
+  return run_finish<MODE>(a, ch, lane, mx, Zr, d, vals);
 }
 
 // Sum of the 64 lanes' run sums in lane order (every lane gets it).
@@ -765,72 +786,146 @@ __device__ __forceinline__ void gather_chunks(const float* src, int n, float (&r
   }
 }
 
-__global__ __launch_bounds__(64) void residual_phase2_kernel(ResidualArgs a) {
-  const int row = blockIdx.x / a.nch, ch = blockIdx.x % a.nch;
-  const int lane = threadIdx.x;
+// Phases 2 and 3 run one wave per 1024-element chunk, kWavesRes chunks to a workgroup (fewer
+// arrivals at each counter: same-address atomics serialize), and the tails on wave 0.
+constexpr int kWavesRes = 4;
+__host__ __device__ constexpr int nq_res(int nch) { return (nch + kWavesRes - 1) / kWavesRes; }
+
+// arrive_last for one wave (the other waves of the workgroup have left).
+__device__ __forceinline__ bool arrive_last_wave(int* cnt, int total) {
+  __builtin_amdgcn_s_waitcnt(0);
+  int last = 0;
+  if ((threadIdx.x & 63) == 0) {
+    const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == total - 1;
+    if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return __builtin_amdgcn_readfirstlane(last) != 0;
+}
+
+__global__ __launch_bounds__(64 * kWavesRes) void residual_phase2_kernel(ResidualArgs a) {
+  const int nq = nq_res(a.nch);
+  const int row = blockIdx.x / nq, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ch = (blockIdx.x % nq) * kWavesRes + wave;
+  const int K = a.M - 1;
+  const int64_t spec_l = lane < K ? a.spec[lane + 1] : -1;  // the finish's drafts, loaded up front
   const float mx = ws_ld(a.rowmax + row);
+  if (ch < a.nch) {
   float vals[kRun];
   const float rs = run_values<0>(a, row, ch, lane, mx, 1.f, vals);
   const float ct = chunk_total(rs);
-  const int K = a.M - 1;
   if (row < K) {
-    const int64_t d = a.spec[row + 1];
+    // the workgroup whose chunk holds draft d keeps e(d) and q(d) for the accept test
+    const int64_t d = __shfl(spec_l, row);
     const int base = ch * kChunk + lane * kRun;
-    if (d >= base && d < base + kRun) ws_st(a.e_draft + row, vals[d - base]);
+    if (d >= base && d < base + kRun) {
+      ws_st(a.e_draft + row, vals[d - base]);
+      ws_st(a.q_draft + row, a.q[(size_t)row * a.V + d]);
+    }
   }
-  if (lane == 0) ws_st(a.chunk_sum + blockIdx.x, ct);
-  if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
+  if (lane == 0) ws_st(a.chunk_sum + (size_t)row * a.nch + ch, ct);
+  }
+  if (!arrive_last(a.cnt_rows + row * kCntStride, nq)) return;
+  if (wave) return;
   float cs[kMaxChunks / 64];
   gather_chunks(a.chunk_sum + (size_t)row * a.nch, a.nch, cs);
   const float Zrow = wave_seq_sum(cs);
   if (lane == 0) ws_st(a.Z + row, Zrow);
-  if (!arrive_last(a.cnt_all, a.M)) return;
-  __shared__ float ed[32], zz[32], qd[32];
-  __shared__ int dvalid[32];
-  ws_gather(a.e_draft, K, ed);
-  ws_gather(a.Z, K, zz);
+  if (!arrive_last_wave(a.cnt_all, a.M)) return;
+  // the accept test, every draft at once (one round trip for its loads): n = the drafts that
+  // pass before the first that fails, where an out-of-vocabulary draft fails
+  bool pass = false;
   if (lane < K) {
-    const int64_t d = a.spec[lane + 1];
-    dvalid[lane] = d >= 0 && d < a.V;  // an out-of-vocabulary draft is rejected
-    qd[lane] = dvalid[lane] ? a.q[(size_t)lane * a.V + d] : 0.f;
+    const float e = ws_ld(a.e_draft + lane), z = ws_ld(a.Z + lane), qv = ws_ld(a.q_draft + lane);
+    const float ul = a.u[lane];
+    const bool ok = spec_l >= 0 && spec_l < a.V;
+    pass = ok && __fmul_rn(ul, qv) < __fdiv_rn(e, z);
   }
-  __syncthreads();
-  if (lane == 0) {
-    int n = 0;
-    while (n < K && dvalid[n] && __fmul_rn(a.u[n], qd[n]) < __fdiv_rn(ed[n], zz[n])) ++n;
-    ws_st(a.n_ws, n);
-  }
+  const unsigned long long m = __ballot(pass);
+  const int n = __builtin_ctzll(~m);  // <= K: lanes from K on do not pass
+  if (lane == 0) ws_st(a.n_ws, n);
 }
 
 // Phase 3: one row j = n (the first rejected draft's row, or the bonus row K): chunk sums of
 // r, then the last workgroup draws the token with u[K] by a blocked inverse-CDF search.
-__global__ __launch_bounds__(64) void residual_phase3_kernel(ResidualArgs a) {
-  __shared__ float pick_s;
-  __shared__ float scratch[kMaxChunks];
-  const int ch = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(ResidualArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ch = blockIdx.x * kWavesRes + wave;
   const int K = a.M - 1;
-  const int j = ws_ld(a.n_ws);
-  const float mx = ws_ld(a.rowmax + j), Zj = ws_ld(a.Z + j);
+  // every row's max and Z are loaded with n (one round trip, not two)
+  const int rl = lane < a.M ? lane : 0;
+  const int n_l = ws_ld(a.n_ws);
+  const float mx_l = ws_ld(a.rowmax + rl), z_l = ws_ld(a.Z + rl);
+  const float uK = a.u[K];
+  const int j = __builtin_amdgcn_readfirstlane(n_l);
+  const float mx = lane_val(mx_l, j), Zj = lane_val(z_l, j);
   float vals[kRun];
+  if (ch < a.nch) {
   const float rs = j < K ? run_values<1>(a, j, ch, lane, mx, Zj, vals) : run_values<2>(a, j, ch, lane, mx, Zj, vals);
   const float ct = chunk_total(rs);
   if (lane == 0) ws_st(a.chunk_sum + ch, ct);
-  if (!arrive_last(a.cnt_all, a.nch)) return;
-  // blocked inverse-CDF search with u[K]: the chunk (first whose running total exceeds the
-  // target, else the last nonzero one), then its run, then the element; every sum sequential
+  }
+  if (!arrive_last(a.cnt_all, gridDim.x)) return;
+  // The last workgroup: wave 0 runs the exact chain over the chunk sums while wave 1 computes
+  // the values and run sums of the chunk that an unordered (parallel) scan finds, which the
+  // exact search lands on in all but rounding ties (wave 0 then computes its own).
+  __shared__ float sp_vals[kChunk], sp_runs[64];
+  __shared__ int sp_chunk;
   float cs[kMaxChunks / 64];
-  gather_chunks(a.chunk_sum, a.nch, cs);
-  const float R = wave_seq_sum(cs);
+  constexpr int RC = kMaxChunks / 64;
+  float pre[RC];
+  if (wave == 1) {
+    gather_chunks(a.chunk_sum, a.nch, cs);
+#pragma unroll
+    for (int k = 0; k < RC; ++k) pre[k] = cs[k];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {  // the RC scans side by side
+#pragma unroll
+      for (int k = 0; k < RC; ++k) {
+        const float y = __shfl_up(pre[k], o);
+        if (lane >= o) pre[k] += y;
+      }
+    }
+    float carry = 0.f;
+#pragma unroll
+    for (int k = 0; k < RC; ++k) {
+      const float t = lane_val(pre[k], 63);
+      pre[k] += carry;
+      carry += t;
+    }
+    float unused;
+    const int c_guess = wave_seq_choose(cs, pre, 0.f, uK * carry, &unused);
+    const int cg = c_guess >= 0 ? c_guess : 0;
+    const float rs = j < K ? run_values<1>(a, j, cg, lane, mx, Zj, vals) : run_values<2>(a, j, cg, lane, mx, Zj, vals);
+#pragma unroll
+    for (int e = 0; e < kRun; ++e) sp_vals[lane * kRun + e] = vals[e];
+    sp_runs[lane] = rs;
+    if (lane == 0) sp_chunk = cg;
+  }
+  if (wave == 0) {
+    gather_chunks(a.chunk_sum, a.nch, cs);
+    wave_seq_prefix(cs, 0.f, pre);  // the exact chain: the running sums, the last the total
+  }
+  __syncthreads();
+  if (wave) return;
+  const float R = lane_val(pre[RC - 1], 63);
   const bool degenerate = !(R > 0.f);
-  const float target = __fmul_rn(a.u[K], R);
+  const float target = __fmul_rn(uK, R);
   int pick = -1;
   if (!degenerate) {
     float acc;
-    const int c = wave_seq_search(cs, 0.f, target, &acc, scratch);
-    const float rsum = j < K ? run_values<1>(a, j, c, lane, mx, Zj, vals) : run_values<2>(a, j, c, lane, mx, Zj, vals);
-    const float rr[1] = {rsum};
+    const int c = wave_seq_choose(cs, pre, 0.f, target, &acc);
+    float rs_l;
+    if (c == sp_chunk) {
+#pragma unroll
+      for (int e = 0; e < kRun; ++e) vals[e] = sp_vals[lane * kRun + e];
+      rs_l = sp_runs[lane];
+    } else {
+      rs_l = j < K ? run_values<1>(a, j, c, lane, mx, Zj, vals) : run_values<2>(a, j, c, lane, mx, Zj, vals);
+    }
+    const float rr[1] = {rs_l};
     float run_acc;
-    const int run = wave_seq_search(rr, acc, target, &run_acc, scratch);
+    const int run = wave_seq_search(rr, acc, target, &run_acc);
     if (lane == run) {
       float x = run_acc;
       int last_nz = -1;
@@ -843,10 +938,8 @@ __global__ __launch_bounds__(64) void residual_phase3_kernel(ResidualArgs a) {
         }
       }
       if (pick < 0) pick = c * kChunk + lane * kRun + last_nz;
-      pick_s = __int_as_float(pick);
     }
-    __syncthreads();
-    pick = __float_as_int(pick_s);
+    pick = __builtin_amdgcn_readlane(pick, run & 63);  // run >= 0: chunk c's sum is positive
   } else {
     // degenerate residual (all zero): the row's argmax, first index on ties (keys are unique)
     const uint16_t* lg = a.logits + (size_t)j * a.V;
@@ -930,7 +1023,7 @@ int nch_run(int V) { return (V + kChunk - 1) / kChunk; }
 size_t scratch_bytes(int M, int V) {
   const size_t argmax = (size_t)M * nch_top(V) * 8 + (size_t)M * 8 + (size_t)M * 4;
   const size_t samp = (size_t)M * nch_top(V) * kCand * 8 + (size_t)M * 8;
-  const size_t resid = (size_t)M * nch_run(V) * 4 + (size_t)M * 4 * 3 + 16;
+  const size_t resid = (size_t)M * nch_run(V) * 4 + (size_t)M * 4 * 4 + 16;
   size_t m = argmax > samp ? argmax : samp;
   m = m > resid + argmax ? m : resid + argmax;
   return (m + 255) & ~(size_t)255;
@@ -1101,14 +1194,15 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
   r += (size_t)M * a.nch * 4;
   a.Z = (float*)r;
   a.e_draft = a.Z + M;
-  a.n_ws = (int*)(a.e_draft + M);
+  a.q_draft = a.e_draft + M;
+  a.n_ws = (int*)(a.q_draft + M);
   a.cnt_rows = w.cnt + 64 * kCntStride;
   a.cnt_all = w.cnt + 96 * kCntStride;
   a.o = make_out(nullptr, n_accepted, tok, pos, slot, tokens, commit);
-  hipLaunchKernelGGL(residual_phase2_kernel, dim3(M * a.nch), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(residual_phase2_kernel, dim3(M * nq_res(a.nch)), dim3(64 * kWavesRes), 0, st, a);
   if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
   a.cnt_all = w.cnt + 128 * kCntStride;
-  hipLaunchKernelGGL(residual_phase3_kernel, dim3(a.nch), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(residual_phase3_kernel, dim3(nq_res(a.nch)), dim3(64 * kWavesRes), 0, st, a);
   return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
