@@ -89,6 +89,49 @@ __device__ __forceinline__ void wave_seq_prefix(const float (&r)[R], float acc, 
 // The sequential inverse-CDF step: the first element whose running sum exceeds target, else the
 // last positive element (-1 if none); *base gets the running sum before it. Uniform result.
 // lds: 64 R floats of scratch.
+// wave_seq_prefix by lane 0 alone over a copy in LDS (lds: 64 R floats, 16-byte aligned, private
+// to the wave): the values go to LDS, lane 0 reads them 16 at a time and runs the chain as plain
+// dependent adds, writing each running sum back in place, and every lane reads its own. No
+// cross-lane move per element.
+template <int R>
+__device__ __forceinline__ void wave_seq_prefix_lds(const float (&r)[R], float acc, float (&pre)[R], float* lds) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < R; ++k) lds[64 * k + lane] = r[k];
+  asm volatile("" ::: "memory");
+  if (lane == 0) {
+    // 32 values a block; the next block's loads are issued (and pinned by the clobber) before
+    // the current block's adds, so that they are in flight meanwhile
+    float4* b = (float4*)lds;
+    constexpr int NB = 8, NQ = 16 * R;
+    float4 cur[NB], nxt[NB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) cur[t] = b[t];
+#pragma unroll
+    for (int q = 0; q < NQ; q += NB) {
+      if (q + NB < NQ) {
+#pragma unroll
+        for (int t = 0; t < NB; ++t) nxt[t] = b[q + NB + t];
+      }
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        acc = __fadd_rn(acc, cur[t].x); cur[t].x = acc;
+        acc = __fadd_rn(acc, cur[t].y); cur[t].y = acc;
+        acc = __fadd_rn(acc, cur[t].z); cur[t].z = acc;
+        acc = __fadd_rn(acc, cur[t].w); cur[t].w = acc;
+      }
+#pragma unroll
+      for (int t = 0; t < NB; ++t) b[q + t] = cur[t];
+#pragma unroll
+      for (int t = 0; t < NB; ++t) cur[t] = nxt[t];
+    }
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int k = 0; k < R; ++k) pre[k] = lds[64 * k + lane];
+  asm volatile("" ::: "memory");
+}
 // Given the running sums pre of r from acc: the first element whose running sum exceeds target,
 // else the last positive element (-1 if none); *base gets the running sum before it. Uniform.
 template <int R>
@@ -741,25 +784,37 @@ __device__ __forceinline__ void run_load(const ResidualArgs& a, int row, int ch,
 // The run's values of r from its loaded data: r = e / Z - q clamped at 0 (residual), or e / Z
 // (bonus), or e (phase 2, Z unused). Returns the sequential run sum.
 template <int MODE>
+__device__ __forceinline__ float r_value(const ResidualArgs& a, int i0, float mx, float Zr, const RunData& d, int e) {
+  float v = 0.f;
+  if (i0 + e < a.V) {
+    v = texp(__fsub_rn(bf16_bits_to_f32((d.lw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), mx));
+    if (MODE >= 1) v = __fdiv_rn(v, Zr);
+    if (MODE == 1) {
+      v = __fsub_rn(v, d.qv[e]);
+      v = v > 0.f ? v : 0.f;
+    }
+  }
+  return v;
+}
+template <int MODE>
 __device__ __forceinline__ float run_finish(const ResidualArgs& a, int ch, int lane, float mx, float Zr, const RunData& d, float (&vals)[kRun]) {
   const int i0 = ch * kChunk + lane * kRun;
-  const float (&qv)[kRun] = d.qv;
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < kRun; ++e) {
-    float v = 0.f;
-    if (i0 + e < a.V) {
-      v = texp(__fsub_rn(bf16_bits_to_f32((d.lw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), mx));
-      if (MODE >= 1) v = __fdiv_rn(v, Zr);
-      if (MODE == 1) {
-        v = __fsub_rn(v, qv[e]);
-        v = v > 0.f ? v : 0.f;
-      }
-    }
-    vals[e] = v;
-    s = __fadd_rn(s, v);
+    vals[e] = r_value<MODE>(a, i0, mx, Zr, d, e);
+    s = __fadd_rn(s, vals[e]);
   }
   return s;
+}
+// Elements [E0, E1) of the run's values into out[e * 64 + lane] (element-major: conflict-free).
+template <int MODE, int E0, int E1>
+__device__ __forceinline__ void run_part(const ResidualArgs& a, int row, int ch, int lane, float mx, float Zr, float* out) {
+  RunData d;
+  run_load<MODE>(a, row, ch, lane, d);
+  const int i0 = ch * kChunk + lane * kRun;
+#pragma unroll
+  for (int e = E0; e < E1; ++e) out[e * 64 + lane] = r_value<MODE>(a, i0, mx, Zr, d, e);
 }
 template <int MODE>
 __device__ __forceinline__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float Zr, float (&vals)[kRun]) {
@@ -866,16 +921,17 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
   if (lane == 0) ws_st(a.chunk_sum + ch, ct);
   }
   if (!arrive_last(a.cnt_all, gridDim.x)) return;
-  // The last workgroup: wave 0 runs the exact chain over the chunk sums while wave 1 computes
-  // the values and run sums of the chunk that an unordered (parallel) scan finds, which the
-  // exact search lands on in all but rounding ties (wave 0 then computes its own).
-  __shared__ float sp_vals[kChunk], sp_runs[64];
+  // The last workgroup: wave 0 runs the exact chain over the chunk sums while waves 1-3 compute
+  // the values of the chunk that an unordered (parallel) scan finds, a third of each run each;
+  // the exact search lands on that chunk in all but rounding ties (wave 0 then computes its own).
+  __shared__ float sp_vals[kChunk];
   __shared__ int sp_chunk;
+  __shared__ __align__(16) float chain_lds[kMaxChunks];
   float cs[kMaxChunks / 64];
   constexpr int RC = kMaxChunks / 64;
   float pre[RC];
-  if (wave == 1) {
-    gather_chunks(a.chunk_sum, a.nch, cs);
+  gather_chunks(a.chunk_sum, a.nch, cs);
+  if (wave) {
 #pragma unroll
     for (int k = 0; k < RC; ++k) pre[k] = cs[k];
 #pragma unroll
@@ -896,15 +952,18 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
     float unused;
     const int c_guess = wave_seq_choose(cs, pre, 0.f, uK * carry, &unused);
     const int cg = c_guess >= 0 ? c_guess : 0;
-    const float rs = j < K ? run_values<1>(a, j, cg, lane, mx, Zj, vals) : run_values<2>(a, j, cg, lane, mx, Zj, vals);
-#pragma unroll
-    for (int e = 0; e < kRun; ++e) sp_vals[lane * kRun + e] = vals[e];
-    sp_runs[lane] = rs;
-    if (lane == 0) sp_chunk = cg;
-  }
-  if (wave == 0) {
-    gather_chunks(a.chunk_sum, a.nch, cs);
-    wave_seq_prefix(cs, 0.f, pre);  // the exact chain: the running sums, the last the total
+    if (j < K) {
+      if (wave == 1) run_part<1, 0, 6>(a, j, cg, lane, mx, Zj, sp_vals);
+      else if (wave == 2) run_part<1, 6, 11>(a, j, cg, lane, mx, Zj, sp_vals);
+      else run_part<1, 11, 16>(a, j, cg, lane, mx, Zj, sp_vals);
+    } else {
+      if (wave == 1) run_part<2, 0, 6>(a, j, cg, lane, mx, Zj, sp_vals);
+      else if (wave == 2) run_part<2, 6, 11>(a, j, cg, lane, mx, Zj, sp_vals);
+      else run_part<2, 11, 16>(a, j, cg, lane, mx, Zj, sp_vals);
+    }
+    if (wave == 1 && lane == 0) sp_chunk = cg;
+  } else {
+    wave_seq_prefix_lds(cs, 0.f, pre, chain_lds);  // the exact chain: the running sums, the last the total
   }
   __syncthreads();
   if (wave) return;
@@ -915,11 +974,13 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
   if (!degenerate) {
     float acc;
     const int c = wave_seq_choose(cs, pre, 0.f, target, &acc);
-    float rs_l;
+    float rs_l = 0.f;
     if (c == sp_chunk) {
 #pragma unroll
-      for (int e = 0; e < kRun; ++e) vals[e] = sp_vals[lane * kRun + e];
-      rs_l = sp_runs[lane];
+      for (int e = 0; e < kRun; ++e) {
+        vals[e] = sp_vals[e * 64 + lane];
+        rs_l = __fadd_rn(rs_l, vals[e]);  // run_finish's sum
+      }
     } else {
       rs_l = j < K ? run_values<1>(a, j, c, lane, mx, Zj, vals) : run_values<2>(a, j, c, lane, mx, Zj, vals);
     }
