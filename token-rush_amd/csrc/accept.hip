@@ -538,7 +538,8 @@ __device__ void merge_lists_top64_thr(const uint32_t* src, int n, uint32_t* out_
 
 // ------------------------------------------------------------------ accept outputs
 
-enum { FIN_NONE = 0, FIN_CHAIN = 1, FIN_TREE = 2 };
+// FIN_KEYS: the per-chunk keys only (no row reduction; the residual kernels reduce them)
+enum { FIN_NONE = 0, FIN_CHAIN = 1, FIN_TREE = 2, FIN_KEYS = 3 };
 
 struct ArgmaxArgs {
   const uint16_t* logits;  // bf16 [M, V]
@@ -593,6 +594,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
     for (int w = 1; w < 4; ++w) best = wmax[w] > best ? wmax[w] : best;
     ws_st(a.keys + blockIdx.x, best);
   }
+  if (a.fin == FIN_KEYS) return;
   if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
   if (threadIdx.x < 64) {
     uint64_t b = 0;
@@ -730,12 +732,13 @@ struct ResidualArgs {
   const int64_t* spec;     // committed + K drafts [K+1]
   const float* u;          // [K+1]
   int M, V, nch;           // M = K + 1 rows, nch = 1024-chunks per row
-  const float* rowmax;     // ws [M] (from argmax_kernel)
+  const uint64_t* keys;    // ws [M * nka]: argmax_kernel's per-chunk (value, index) keys
+  int nka;                 // keys per row (<= 64)
+  float* rowmax;           // ws [M]: row maxima, stored by phase 2
   float* chunk_sum;        // ws [M * nch] (phase 2), then [nch] (phase 3)
   float* Z;                // ws [M]
   float* e_draft;          // ws [M]
   float* q_draft;          // ws [M]: q_i(d_i), stored by the workgroup whose chunk holds d_i
-  int* n_ws;               // ws [1]: accepted drafts, read by phase 3
   int* cnt_rows;
   int* cnt_all;
   AcceptOut o;
@@ -864,7 +867,9 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase2_kernel(Residua
   const int ch = (blockIdx.x % nq) * kWavesRes + wave;
   const int K = a.M - 1;
   const int64_t spec_l = lane < K ? a.spec[lane + 1] : -1;  // the finish's drafts, loaded up front
-  const float mx = ws_ld(a.rowmax + row);
+  // the row maximum from the argmax kernel's chunk keys (one per lane)
+  const uint64_t key = ws_ld(a.keys + (size_t)row * a.nka + (lane < a.nka ? lane : a.nka - 1));
+  const float mx = bf16_bits_to_f32(unord16((uint32_t)(wave_max_u64(key) >> 32)));
   if (ch < a.nch) {
   float vals[kRun];
   const float rs = run_values<0>(a, row, ch, lane, mx, 1.f, vals);
@@ -885,20 +890,10 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase2_kernel(Residua
   float cs[kMaxChunks / 64];
   gather_chunks(a.chunk_sum + (size_t)row * a.nch, a.nch, cs);
   const float Zrow = wave_seq_sum(cs);
-  if (lane == 0) ws_st(a.Z + row, Zrow);
-  if (!arrive_last_wave(a.cnt_all, a.M)) return;
-  // the accept test, every draft at once (one round trip for its loads): n = the drafts that
-  // pass before the first that fails, where an out-of-vocabulary draft fails
-  bool pass = false;
-  if (lane < K) {
-    const float e = ws_ld(a.e_draft + lane), z = ws_ld(a.Z + lane), qv = ws_ld(a.q_draft + lane);
-    const float ul = a.u[lane];
-    const bool ok = spec_l >= 0 && spec_l < a.V;
-    pass = ok && __fmul_rn(ul, qv) < __fdiv_rn(e, z);
+  if (lane == 0) {
+    ws_st(a.Z + row, Zrow);
+    ws_st(a.rowmax + row, mx);
   }
-  const unsigned long long m = __ballot(pass);
-  const int n = __builtin_ctzll(~m);  // <= K: lanes from K on do not pass
-  if (lane == 0) ws_st(a.n_ws, n);
 }
 
 // Phase 3: one row j = n (the first rejected draft's row, or the bonus row K): chunk sums of
@@ -907,12 +902,16 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ch = blockIdx.x * kWavesRes + wave;
   const int K = a.M - 1;
-  // every row's max and Z are loaded with n (one round trip, not two)
-  const int rl = lane < a.M ? lane : 0;
-  const int n_l = ws_ld(a.n_ws);
+  // The accept test, every draft at once, in every wave (one round trip for all its loads and
+  // every row's max and Z): n = the drafts that pass before the first that fails, where an
+  // out-of-vocabulary draft fails.
+  const int rl = lane < a.M ? lane : 0, dl = lane < K ? lane : 0;
   const float mx_l = ws_ld(a.rowmax + rl), z_l = ws_ld(a.Z + rl);
+  const float e_l = ws_ld(a.e_draft + dl), q_l = ws_ld(a.q_draft + dl), u_l = a.u[dl];
+  const int64_t d_l = a.spec[dl + 1];
   const float uK = a.u[K];
-  const int j = __builtin_amdgcn_readfirstlane(n_l);
+  const bool pass = lane < K && d_l >= 0 && d_l < a.V && __fmul_rn(u_l, q_l) < __fdiv_rn(e_l, z_l);
+  const int j = __builtin_ctzll(~__ballot(pass));  // <= K: lanes from K on do not pass
   const float mx = lane_val(mx_l, j), Zj = lane_val(z_l, j);
   float vals[kRun];
   if (ch < a.nch) {
@@ -1238,7 +1237,7 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
   // phase 1: row maxima (argmax kernel, no finish)
   const size_t am = (size_t)M * nch_top(V) * 8 + (size_t)M * 8;
   float* rowmax = (float*)(w.scratch + am);
-  int rc = launch_argmax(logits, M, V, FIN_NONE, nullptr, nullptr, w, rowmax,
+  int rc = launch_argmax(logits, M, V, FIN_KEYS, nullptr, nullptr, w, nullptr,
                          make_out(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr), st);
   if (rc) return rc;
   ResidualArgs a;
@@ -1249,6 +1248,8 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
   a.M = M;
   a.V = V;
   a.nch = nch_run(V);
+  a.keys = (const uint64_t*)w.scratch;
+  a.nka = nch_arg(V, M);
   a.rowmax = rowmax;
   char* r = w.scratch + am + (size_t)M * 4;
   a.chunk_sum = (float*)r;
@@ -1256,7 +1257,6 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
   a.Z = (float*)r;
   a.e_draft = a.Z + M;
   a.q_draft = a.e_draft + M;
-  a.n_ws = (int*)(a.q_draft + M);
   a.cnt_rows = w.cnt + 64 * kCntStride;
   a.cnt_all = w.cnt + 96 * kCntStride;
   a.o = make_out(nullptr, n_accepted, tok, pos, slot, tokens, commit);
