@@ -44,7 +44,8 @@ __device__ __forceinline__ void ws_gather(const T* src, int n, T* dst) {
 // The same fixed left-to-right fp32 chains, run by a whole wave over values held in registers:
 // element j of the sequence is lane j % 64 of r[j / 64]. v_readlane brings each element to a
 // scalar register in index order, so every lane computes exactly the sequential result, without
-// a memory or LDS round trip per element (a lane-0 loop over LDS costs ~70 ns per element).
+// a memory or LDS round trip per element (a lane-0 loop that waits for an LDS load per element
+// costs ~70 ns per element; wave_seq_prefix below loads its blocks ahead).
 // Callers pass zeros past the sequence's end: the chains are over non-negative values, to which
 // adding +0 changes nothing, so no per-element bound check (a divergent branch) is needed.
 __device__ __forceinline__ float lane_val(float v, int i) {
@@ -68,33 +69,12 @@ __device__ __forceinline__ float wave_seq_sum(const float (&r)[R]) {
   return s;
 }
 // Running sums acc + x_0 + ... + x_j (left to right): lane i of pre[k] gets element 64 k + i's.
-// The chain is the one above; each sum is placed into its lane with v_writelane (a store of the
-// same word by all 64 lanes at every step, then a read back, took twice the chain's time).
+// Lane 0 alone runs the chain over a copy in LDS (lds: 64 R floats, 16-byte aligned, private to
+// the wave): the values go to LDS, lane 0 reads them back in blocks and runs the chain as plain
+// dependent adds, writing each running sum in place, and every lane reads its own. (Chains on
+// v_readlane with each sum selected into its lane cost about twice as much per element.)
 template <int R>
-__device__ __forceinline__ void wave_seq_prefix(const float (&r)[R], float acc, float (&pre)[R]) {
-#pragma unroll
-  for (int k = 0; k < R; ++k) {
-    float x = r[k];
-    int p = 0;
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      if ((i & 15) == 0) asm volatile("" : "+v"(x), "+v"(acc), "+v"(p));
-      acc = __fadd_rn(acc, lane_val(x, i));
-      p = lane == i ? __float_as_int(acc) : p;
-    }
-    pre[k] = __int_as_float(p);
-  }
-}
-// The sequential inverse-CDF step: the first element whose running sum exceeds target, else the
-// last positive element (-1 if none); *base gets the running sum before it. Uniform result.
-// lds: 64 R floats of scratch.
-// wave_seq_prefix by lane 0 alone over a copy in LDS (lds: 64 R floats, 16-byte aligned, private
-// to the wave): the values go to LDS, lane 0 reads them 16 at a time and runs the chain as plain
-// dependent adds, writing each running sum back in place, and every lane reads its own. No
-// cross-lane move per element.
-template <int R>
-__device__ __forceinline__ void wave_seq_prefix_lds(const float (&r)[R], float acc, float (&pre)[R], float* lds) {
+__device__ __forceinline__ void wave_seq_prefix(const float (&r)[R], float acc, float (&pre)[R], float* lds) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int k = 0; k < R; ++k) lds[64 * k + lane] = r[k];
@@ -161,9 +141,9 @@ __device__ __forceinline__ int wave_seq_choose(const float (&r)[R], const float 
 }
 // The sequential inverse-CDF step over r from acc (wave_seq_choose of wave_seq_prefix).
 template <int R>
-__device__ __forceinline__ int wave_seq_search(const float (&r)[R], float acc, float target, float* base) {
+__device__ __forceinline__ int wave_seq_search(const float (&r)[R], float acc, float target, float* base, float* lds) {
   float pre[R];
-  wave_seq_prefix(r, acc, pre);
+  wave_seq_prefix(r, acc, pre, lds);
   return wave_seq_choose(r, pre, acc, target, base);
 }
 
@@ -656,13 +636,14 @@ __device__ int64_t sample_pick(const uint32_t* tk, const uint32_t* ti, float T, 
   const float er[1] = {e};
   const float p = __fdiv_rn(e, wave_seq_sum(er));
   // cumulative sums in rank order; lane i keeps the sum through rank i
+  __shared__ __align__(16) float cum_s[64];
   const float pr[1] = {p};
   float cum[1];
-  wave_seq_prefix(pr, 0.f, cum);
+  wave_seq_prefix(pr, 0.f, cum, cum_s);
   const bool keep = __fsub_rn(cum[0], p) < top_p && i < top_k;
   const float pk[1] = {keep ? p : 0.f};
   float cum2[1];
-  wave_seq_prefix(pk, 0.f, cum2);
+  wave_seq_prefix(pk, 0.f, cum2, cum_s);
   const float target = __fmul_rn(u, lane_val(cum2[0], kCand - 1));
   const float mycum2 = cum2[0];
   const unsigned long long below = __ballot(mycum2 < target);
@@ -962,7 +943,7 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
     }
     if (wave == 1 && lane == 0) sp_chunk = cg;
   } else {
-    wave_seq_prefix_lds(cs, 0.f, pre, chain_lds);  // the exact chain: the running sums, the last the total
+    wave_seq_prefix(cs, 0.f, pre, chain_lds);  // the exact chain: the running sums, the last the total
   }
   __syncthreads();
   if (wave) return;
@@ -985,7 +966,7 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
     }
     const float rr[1] = {rs_l};
     float run_acc;
-    const int run = wave_seq_search(rr, acc, target, &run_acc);
+    const int run = wave_seq_search(rr, acc, target, &run_acc, chain_lds);
     if (lane == run) {
       float x = run_acc;
       int last_nz = -1;
