@@ -327,17 +327,18 @@ __device__ __forceinline__ uint32_t wave_kth(const uint32_t (&kv)[R]) {
 }
 
 // The top 64 of n <= kTopCap candidate keys (vkey()s) in LDS, by rank: thread t compares
-// candidate t % kTopCap with one half of the others, the halves' counts meet in rank[] (zeroed
-// by the caller), and the candidates of rank < 64 land at their rank. 256 threads.
+// candidate t % kTopCap with one half of the n (rounded up to 8) slots, the halves' counts meet
+// in rank[] (zeroed by the caller), and the candidates of rank < 64 land at their rank. 256
+// threads.
 constexpr int kTopCap = 128;
 __device__ void lds_rank_top64(const uint64_t* kk, int n, int* rank, uint32_t* out_k, uint32_t* out_i) {
   const int tid = threadIdx.x, c = tid & (kTopCap - 1), half = tid >> 7;
   if (c < n) {
     const uint64_t key = kk[c];
     int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-    const int j0 = half * (kTopCap / 2);
-#pragma unroll
-    for (int j = 0; j < kTopCap / 2; j += 4) {  // slots past n hold 0: below every key
+    const int h = ((n + 7) >> 3) << 2;  // half of n rounded up to 8: 2 h <= kTopCap
+    const int j0 = half * h;
+    for (int j = 0; j < h; j += 4) {  // slots past n hold 0: below every key
       r0 += kk[j0 + j] > key;
       r1 += kk[j0 + j + 1] > key;
       r2 += kk[j0 + j + 2] > key;
@@ -481,20 +482,23 @@ __device__ void merge_lists_top64(const uint32_t* src, int n, uint32_t* out_k, u
 // the 64th largest of the lists' first four keys bounds the row's 64th largest from below; the
 // entries >= tau (a prefix of each list, typically ~70 in all) are ranked as in
 // select_top64_thr. More than kTopCap of them take merge_lists_top64 instead; both give the same
-// list. Wave w loads ranks 16 w .. 16 w + 15 of list `lane`, all loads issued at once.
+// list. Load j of wave w brings list 4 j + w, rank `lane` (one list per load: 4 cache lines,
+// where a list per lane touched 64), all loads issued at once; the lists' first four keys
+// meet in LDS for tau.
 __device__ void merge_lists_top64_thr(const uint32_t* src, int n, uint32_t* out_k, uint32_t* out_i) {
   constexpr int kR = 16;
   __shared__ uint64_t kk[kTopCap];
   __shared__ int rank[kTopCap];
+  __shared__ uint32_t heads[4 * kCand];
   __shared__ uint32_t s_tau;
   __shared__ int s_cnt;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int c = lane < n ? lane : n - 1;
   uint32_t kv[kR], iv[kR];
 #pragma unroll
   for (int j = 0; j < kR; ++j) {
-    const uint64_t v = ws_ld((const uint64_t*)(src + (size_t)c * kCand * 2 + 2 * (kR * wid + j)));
-    kv[j] = lane < n ? (uint32_t)v : 0u;
+    const int c = 4 * j + wid;  // list
+    const uint64_t v = ws_ld((const uint64_t*)(src + (size_t)(c < n ? c : n - 1) * kCand * 2 + 2 * lane));
+    kv[j] = c < n ? (uint32_t)v : 0u;
     iv[j] = (uint32_t)(v >> 32);
   }
   if (tid < kTopCap) {
@@ -502,8 +506,13 @@ __device__ void merge_lists_top64_thr(const uint32_t* src, int n, uint32_t* out_
     rank[tid] = 0;
   }
   if (tid == 0) s_cnt = 0;
+  if (lane < 4) {
+#pragma unroll
+    for (int j = 0; j < kR; ++j) heads[4 * (4 * j + wid) + lane] = kv[j];
+  }
+  __syncthreads();
   if (wid == 0) {
-    const uint32_t head[4] = {kv[0], kv[1], kv[2], kv[3]};
+    const uint32_t head[4] = {heads[lane], heads[64 + lane], heads[128 + lane], heads[192 + lane]};
     const uint32_t v = wave_kth<kCand>(head);
     if (lane == 0) s_tau = v;
   }

@@ -223,7 +223,7 @@ struct GemmArgs {
   // Fused argmax (S == 1): per-row (value, first index) max of the bf16 outputs; the last
   // workgroup reduces the per-workgroup keys and finishes the greedy accept when spec != null.
   int argmax;
-  uint64_t* am_keys;      // [grid, M] workspace
+  uint64_t* am_keys;      // [M, grid] workspace
   int* am_cnt;            // arrival counter, zero between calls
   const int64_t* spec;    // [M] committed token + drafts, or null (argmax only)
   AcceptOut o;            // o.pred [M] always; the rest when spec != null
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     // Publish this workgroup's row keys; the last workgroup reduces them (fixed order is not
     // needed: a max of unique keys) and finishes the accept.
     __syncthreads();
-    if (threadIdx.x < a.M) ws_st(a.am_keys + (size_t)blockIdx.x * a.M + threadIdx.x, rowbest[threadIdx.x]);
+    if (threadIdx.x < a.M) ws_st(a.am_keys + (size_t)threadIdx.x * gridDim.x + blockIdx.x, rowbest[threadIdx.x]);
     if (!arrive_last(a.am_cnt, gridDim.x)) return;
     __shared__ int64_t pred[32], spec[32];
     const int nwv = blockDim.x >> 6;
@@ -482,7 +482,7 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const int g = g0 + lane + 64 * q;
-          k[q] = ws_ld(a.am_keys + (size_t)(g < grid ? g : grid - 1) * a.M + m);
+          k[q] = ws_ld(a.am_keys + (size_t)m * grid + (g < grid ? g : grid - 1));  // lanes on consecutive keys
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q) best = (g0 + lane + 64 * q < grid && k[q] > best) ? k[q] : best;
