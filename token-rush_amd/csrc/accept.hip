@@ -357,28 +357,34 @@ __device__ void lds_rank_top64(const uint64_t* kk, int n, int* rank, uint32_t* o
   __syncthreads();
 }
 
-// Appends this thread's items with keys >= tau (flags[e]) to kk[] as vkey()s: positions from
-// per-item ballots within the wave, one LDS atomic per wave for the wave's base. Returns the
-// total after a barrier (uniform); nothing is written when it exceeds kTopCap.
+// Appends this thread's items with keys >= tau to kk[] as vkey()s. Each thread counts its items;
+// the exclusive prefix of the counts over the wave comes from one ballot per count bit, and one LDS atomic per wave places the wave. Returns the total after a
+// barrier (uniform); nothing is written when it exceeds kTopCap.
 template <int E>
 __device__ int lds_append_keys(const uint32_t (&k16)[E], const uint32_t (&idx)[E], uint32_t tau, uint64_t* kk, int* cnt) {
+  static_assert(E < 64, "per-thread counts must fit six bits");
+  constexpr int kBits = E < 32 ? 5 : 6;
   const int lane = threadIdx.x & 63;
-  int wtot = 0;
+  int c = 0;
 #pragma unroll
-  for (int e = 0; e < E; ++e) wtot += __popcll(__ballot(k16[e] >= tau));
+  for (int e = 0; e < E; ++e) c += k16[e] >= tau ? 1 : 0;
+  int pre = 0, wtot = 0;
+#pragma unroll
+  for (int b = 0; b < kBits; ++b) {
+    const unsigned long long m = __ballot((c >> b) & 1);
+    pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << b;
+    wtot += __popcll(m) << b;
+  }
   int base = 0;
   if (lane == 0 && wtot) base = atomicAdd(cnt, wtot);
-  base = __shfl(base, 0);
+  base = __builtin_amdgcn_readfirstlane(base);
   __syncthreads();
   const int tot = *cnt;
   if (tot <= kTopCap) {
+    int pos = base + pre;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const unsigned long long m = __ballot(k16[e] >= tau);
-      if (k16[e] >= tau) kk[base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] =
-          vkey(k16[e], idx[e]);
-      base += __popcll(m);
-    }
+    for (int e = 0; e < E; ++e)
+      if (k16[e] >= tau) kk[pos++] = vkey(k16[e], idx[e]);
   }
   __syncthreads();
   return tot;
@@ -1067,11 +1073,13 @@ constexpr size_t kCntBytes = 160 * kCntStride * sizeof(int);
 
 int nch_top(int V) { return (V + kTopChunk - 1) / kTopChunk; }
 int arg_chunk(int M) { return M <= 8 ? kArgChunkSmall : kArgChunkLarge; }
-int nch_arg(int V, int M) { return (V + arg_chunk(M) - 1) / arg_chunk(M); }  // <= nch_top: fits its workspace
+int nch_arg(int V, int M) { return (V + arg_chunk(M) - 1) / arg_chunk(M); }
 int nch_run(int V) { return (V + kChunk - 1) / kChunk; }
+// the argmax kernel's chunk keys [M * nch_arg] and row predictions [M]
+size_t argmax_bytes(int M, int V) { return (size_t)M * nch_arg(V, M) * 8 + (size_t)M * 8; }
 
 size_t scratch_bytes(int M, int V) {
-  const size_t argmax = (size_t)M * nch_top(V) * 8 + (size_t)M * 8 + (size_t)M * 4;
+  const size_t argmax = argmax_bytes(M, V) + (size_t)M * 4;
   const size_t samp = (size_t)M * nch_top(V) * kCand * 8 + (size_t)M * 8;
   const size_t resid = (size_t)M * nch_run(V) * 4 + (size_t)M * 4 * 4 + 16;
   size_t m = argmax > samp ? argmax : samp;
@@ -1091,7 +1099,9 @@ bool ws_view(void* ws, size_t bytes, int M, int V, WsView* v) {
   return true;
 }
 
-bool check_mv(int M, int V) { return M >= 1 && M <= 32 && V >= kCand && nch_top(V) <= 64; }
+// V <= 262144: at most 64 argmax chunk keys per row (one per lane of the reducing wave) and at
+// most 64 top-64 lists per row
+bool check_mv(int M, int V) { return M >= 1 && M <= 32 && V >= kCand && nch_arg(V, 1) <= 64 && nch_top(V) <= 64; }
 
 AcceptOut make_out(int64_t* pred, int64_t* n, int64_t* tok, int64_t* pos, int64_t* slot, int64_t* tokens,
                    int64_t* commit) {
@@ -1225,7 +1235,7 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
     return TR_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   // phase 1: row maxima (argmax kernel, no finish)
-  const size_t am = (size_t)M * nch_top(V) * 8 + (size_t)M * 8;
+  const size_t am = argmax_bytes(M, V);
   float* rowmax = (float*)(w.scratch + am);
   int rc = launch_argmax(logits, M, V, FIN_KEYS, nullptr, nullptr, w, nullptr,
                          make_out(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr), st);
