@@ -720,8 +720,10 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
 
 // ------------------------------------------------------------------ residual rejection sampling
 
-// Phase 2: per (row, 1024-chunk) run and chunk sums of e = texp(l - rowmax); per row Z; then
-// the accept tests u_i q_i(d_i) < e_i(d_i) / Z_i.
+// Phase 1 is argmax_kernel storing its per-chunk keys (FIN_KEYS). Phase 2: the row maxima from
+// those keys; per (row, 1024-chunk) run and chunk sums of e = texp(l - rowmax), e(d_i) and
+// q_i(d_i) kept by the chunk holding draft d_i; per row Z and the row maximum. Phase 3: the
+// accept tests u_i q_i(d_i) < e_i(d_i) / Z_i (in every wave), then the draw from row n.
 struct ResidualArgs {
   const uint16_t* logits;  // [K+1, V]
   const float* q;          // [K, V]
@@ -892,8 +894,9 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase2_kernel(Residua
   }
 }
 
-// Phase 3: one row j = n (the first rejected draft's row, or the bonus row K): chunk sums of
-// r, then the last workgroup draws the token with u[K] by a blocked inverse-CDF search.
+// Phase 3: n from the accept tests, then one row j = n (the first rejected draft's row, or the
+// bonus row K): chunk sums of r, then the last workgroup draws the token with u[K] by a blocked
+// inverse-CDF search.
 __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(ResidualArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ch = blockIdx.x * kWavesRes + wave;
@@ -1117,7 +1120,7 @@ AcceptOut make_out(int64_t* pred, int64_t* n, int64_t* tok, int64_t* pos, int64_
 }
 
 // counters (in units of kCntStride ints): [0, 32) rows of the first kernel, [32] all-rows of
-// the first kernel, [64, 96) rows of the residual phase 2, [96] its all-rows, [128] phase 3.
+// the first kernel, [64, 96) rows of the residual phase 2, [128] phase 3.
 int launch_argmax(const void* logits, int M, int V, int fin, const int64_t* spec, const int32_t* parent,
                   const WsView& w, float* rowmax, const AcceptOut& o, hipStream_t st) {
   ArgmaxArgs a;
@@ -1234,7 +1237,7 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
       !ws_view(ws, ws_bytes, M, V, &w))
     return TR_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
-  // phase 1: row maxima (argmax kernel, no finish)
+  // phase 1: the argmax kernel's per-chunk keys (phase 2 reduces them to row maxima)
   const size_t am = argmax_bytes(M, V);
   float* rowmax = (float*)(w.scratch + am);
   int rc = launch_argmax(logits, M, V, FIN_KEYS, nullptr, nullptr, w, nullptr,
@@ -1258,7 +1261,7 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
   a.e_draft = a.Z + M;
   a.q_draft = a.e_draft + M;
   a.cnt_rows = w.cnt + 64 * kCntStride;
-  a.cnt_all = w.cnt + 96 * kCntStride;
+  a.cnt_all = nullptr;  // phase 2 has no all-rows handshake
   a.o = make_out(nullptr, n_accepted, tok, pos, slot, tokens, commit);
   hipLaunchKernelGGL(residual_phase2_kernel, dim3(M * nq_res(a.nch)), dim3(64 * kWavesRes), 0, st, a);
   if (hipGetLastError() != hipSuccess) return TR_ERR_LAUNCH;
