@@ -10,7 +10,8 @@
 //   o2 = bf16(bf16(x2 c) + bf16(x1 s)). q is written bf16; k and the raw v go to cache row
 //   pos + t as fp8(x / sc) with sc = max(amax(x), 1e-6) / 448.
 //   attention: query t of head h sees cache rows <= pos + t; scores q . bf16(k8 * ksc) / sqrt(D);
-//   online softmax in fp32 with l summed before the value scale, P = bf16(p * vsc), acc += P v8;
+//   online softmax in fp32 (base 2 on the device: maxima and exponents in log2 units) with l
+//   summed before the value scale, P = bf16(p * vsc), acc += P v8;
 //   splits combined by their maxima; o = bf16(acc / l) * bf16(sigmoid(gate)), bf16 out.
 //
 // MI355X layout of the split kernel: one workgroup of four waves per (kv head, split); the
@@ -33,6 +34,7 @@ constexpr int kAttnWaves = 4;
 constexpr int kKPitch = kAttnD + 8;     // bf16 elements per K row in LDS
 constexpr int kVPitch = kAttnBlk + 4;   // bf16 elements per V^T row (one d) in LDS
 constexpr float kFp8Max = 448.f;
+constexpr float kLog2e = 1.4426950408889634f;  // scores are kept in log2 units: p = 2^(s - m)
 constexpr int kMaxSplit = 256;  // key-range splits of one flash-decoding call
 static_assert(kMaxSplit <= kAttnD, "the combine kernel gives each split one thread");
 
@@ -359,7 +361,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
       }
       st[kt] = c;
     }
-    // mask, online softmax (this lane: one row, 8 keys)
+    // mask, online softmax (this lane: one row, 8 keys), in log2 units: p = 2^(s - m) by
+    // v_exp_f32 (one instruction where expf takes a range reduction)
+    const float sl2 = a.scale * kLog2e;
     float sc[8];
     float mx = -INFINITY;
     // a block of committed rows only (all before pos) needs no mask; in the others key rel =
@@ -374,26 +378,35 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
         const bool allowed =
             TREE ? rvalid && (committed || (rel < a.M && (rel < 0 || ((vis >> rel) & 1u))))
                  : rvalid && key0 + 16 * kt + 4 * (lane >> 4) + r < L && key0 + 16 * kt + 4 * (lane >> 4) + r <= qlimit;
-        const float v = allowed ? st[kt][r] * a.scale : -INFINITY;
+        const float v = allowed ? st[kt][r] * sl2 : -INFINITY;
         sc[4 * kt + r] = v;
         mx = fmaxf(mx, v);
       }
     mx = max_x32(max_x16(mx));
-    const float m_new = fmaxf(m_i, mx);
-    const float m_safe = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = expf(m_i - m_safe);
+    // Lazy rescale: the rows move to their new maxima (and O^T, l are scaled) only when some row
+    // of the wave gains more than kLazyMax (log2 units) over its running max; otherwise the block
+    // is summed against the running max, so p <= 2^kLazyMax. m, l and O^T stay consistent.
+    constexpr float kLazyMax = 8.f;
+    if (__ballot(mx > m_i + kLazyMax)) {  // uniform; a first finite maximum always counts
+      const float m_new = fmaxf(m_i, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_i - (m_new == -INFINITY ? 0.f : m_new));
+      m_i = m_new;
+      l_i *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) acc[dt] = acc[dt] * alpha;
+    }
+    const float m_safe = m_i == -INFINITY ? 0.f : m_i;
     float psum = 0.f;
     uint32_t pb[4];
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
-      const float p0 = expf(sc[i] - m_safe), p1 = expf(sc[i + 1] - m_safe);
+      const float p0 = __builtin_amdgcn_exp2f(sc[i] - m_safe), p1 = __builtin_amdgcn_exp2f(sc[i + 1] - m_safe);
       psum += p0 + p1;
       const int k0 = 16 * (i / 4) + 4 * (lane >> 4) + (i & 3);
       pb[i / 2] = pk_bf16(p0 * vsc[k0], p1 * vsc[k0 + 1]);
     }
     psum = sum_x32(sum_x16(psum));
-    l_i = l_i * alpha + psum;
-    m_i = m_new;
+    l_i += psum;
     // O^T += V^T P^T: k-index 8 (l / 16) + i <-> key 4 (l / 16) + i (i < 4), 16 + 4 (l / 16) + i - 4
     const bf16x8 pB = __builtin_bit_cast(bf16x8, make_uint4(pb[0], pb[1], pb[2], pb[3]));
     const int vk = 4 * (lane >> 4);
@@ -401,7 +414,6 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
     for (int dt = 0; dt < 16; ++dt) {
       const uint16_t* vr = Vt + (16 * dt + (lane & 15)) * kVPitch;
       const uint2 lo = *(const uint2*)(vr + vk), hi = *(const uint2*)(vr + 16 + vk);
-      acc[dt] = acc[dt] * alpha;
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y)),
                                                         pB, acc[dt], 0, 0, 0);
     }
@@ -455,7 +467,7 @@ __global__ __launch_bounds__(kAttnD) void attn_reduce_kernel(AttnReduceArgs a) {
   if (lane == 0) red[wave] = mm;
   __syncthreads();
   mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float w = mine && m_s != -INFINITY ? expf(m_s - mm) : 0.f;
+  const float w = mine && m_s != -INFINITY ? __builtin_amdgcn_exp2f(m_s - mm) : 0.f;  // maxima in log2 units
   if (mine) wsh[d] = w;
   // total weight sum_s w_s l_s
   float lt = sum_wave(w * l_s);
