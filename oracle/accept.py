@@ -23,8 +23,13 @@ Fixed arithmetic, shared bit-for-bit with the HIP kernels (token-rush_amd/csrc/a
     gives 0. Every operation is one fp32 rounding (no fused multiply-add).
   * Sums over the 64 candidates are sequential in rank order.
   * Sums over a vocabulary row are "blocked": sequential within runs of 16 elements,
-    sequential over the 64 runs of each 1024-element chunk, sequential over chunks (the row
-    is zero-padded to a multiple of 1024; adding +0.0 changes nothing).
+    sequential over the 64 runs of each 1024-element chunk, sequential over the 4 chunks of a
+    group, sequential over groups (the row is zero-padded to whole groups; adding +0.0 changes
+    nothing). The inverse-CDF search descends the same levels.
+  * The residual path's exponentials are taken per chunk: with m_c the chunk's maximum and M
+    the row's, e = fl(texp(l - m_c) * texp(m_c - M)) (flushed to 0 below the smallest normal),
+    and Z sums the chunks as fl(texp(m_c - M) * A_c), A_c the chunk's blocked sum of
+    texp(l - m_c). No pass over the row has to wait for the row maximum.
 
 Pinning (tests/test_oracle_accept.py): texp against numpy's exp (relative error < 2e-7);
 argmax/top64 against numpy argmax/lexsort; sample against brute-force cases, torch's own
@@ -40,7 +45,8 @@ from .int4 import bf16_bits_to_f32
 
 F = np.float32
 CANDIDATES = 64
-RUN, CHUNK = 16, 1024
+RUN, CHUNK, GROUP = 16, 1024, 4
+FLT_MIN = np.finfo(np.float32).tiny            # smallest normal fp32
 
 
 def _f(bits: int) -> np.float32:
@@ -136,61 +142,90 @@ def verify_chain(pred: np.ndarray, spec_toks: np.ndarray, pos: int, slot: int = 
 
 # ------------------------------------------------------------------ blocked reductions
 
-def _padded(row: np.ndarray) -> np.ndarray:
+def _padded(row: np.ndarray, fill=0.0) -> np.ndarray:
     V = row.shape[0]
     Vp = -(-V // CHUNK) * CHUNK
-    out = np.zeros(Vp, dtype=F)
+    out = np.full(Vp, fill, dtype=F)
     out[:V] = row
     return out
 
 
-def blocked_parts(row: np.ndarray):
-    """(run totals [nchunks, 64], chunk totals [nchunks], chunk prefixes [nchunks + 1])."""
-    r = _padded(row).reshape(-1, CHUNK // RUN, RUN)
-    runs = np.cumsum(r, axis=-1, dtype=F)[..., -1]
+def _run_chunk_sums(x: np.ndarray):
+    """x [nchunks, CHUNK] -> (run totals [nchunks, 64], chunk totals [nchunks])."""
+    runs = np.cumsum(x.reshape(x.shape[0], CHUNK // RUN, RUN), axis=-1, dtype=F)[..., -1]
     chunks = np.cumsum(runs, axis=-1, dtype=F)[:, -1]
-    pref = np.concatenate([[F(0.0)], np.cumsum(chunks, dtype=F)]).astype(F)
-    return runs.astype(F), chunks.astype(F), pref
+    return runs.astype(F), chunks.astype(F)
+
+
+def group_parts(chunks: np.ndarray):
+    """Chunk totals -> (group totals [ngroups], group prefixes [ngroups + 1]): sequential over
+    the 4 chunks of a group (zero chunks pad the last group), then over groups."""
+    ng = -(-chunks.shape[0] // GROUP)
+    cp = np.zeros(ng * GROUP, F)
+    cp[:chunks.shape[0]] = chunks
+    groups = np.cumsum(cp.reshape(ng, GROUP), axis=-1, dtype=F)[:, -1].astype(F)
+    pref = np.concatenate([[F(0.0)], np.cumsum(groups, dtype=F)]).astype(F)
+    return groups, pref
+
+
+def blocked_parts(row: np.ndarray):
+    """(run totals [nchunks, 64], chunk totals [nchunks], group totals, group prefixes)."""
+    runs, chunks = _run_chunk_sums(_padded(row).reshape(-1, CHUNK))
+    groups, pref = group_parts(chunks)
+    return runs, chunks, groups, pref
 
 
 def blocked_sum(row: np.ndarray) -> np.float32:
-    return blocked_parts(row)[2][-1]
+    return blocked_parts(row)[3][-1]
+
+
+def _level(acc, parts, target):
+    """One level of the search: the first part whose running sum from acc exceeds target, else
+    the last positive part; returns (index, running sum before it)."""
+    a = acc
+    for i, v in enumerate(parts):
+        if F(a + v) > target:
+            return i, a
+        a = F(a + v)
+    i = max(i for i, v in enumerate(parts) if v > 0)
+    a = acc
+    for v in parts[:i]:
+        a = F(a + v)
+    return i, a
 
 
 def blocked_search(row: np.ndarray, target: np.float32) -> int:
-    """First index whose blocked running sum exceeds target; when rounding leaves none, the
-    last nonzero element of the last nonzero run of the last nonzero chunk."""
-    runs, chunks, pref = blocked_parts(row)
+    """First index whose blocked running sum exceeds target, found level by level (group, its
+    chunks, the chunk's runs, the run's elements); at each level, when rounding leaves no
+    crossing, the last positive part."""
+    runs, chunks, groups, pref = blocked_parts(row)
     pr = _padded(row)
     nch = chunks.shape[0]
-    c = next((c for c in range(nch) if F(pref[c] + chunks[c]) > target), None)
-    if c is None:
-        c = max(c for c in range(nch) if chunks[c] > 0)
-    acc = pref[c]
-    t = None
-    for tt in range(CHUNK // RUN):
-        if F(acc + runs[c, tt]) > target:
-            t = tt
-            break
-        acc = F(acc + runs[c, tt])
-    if t is None:
-        t = max(tt for tt in range(CHUNK // RUN) if runs[c, tt] > 0)
-        acc = pref[c]
-        for tt in range(t):
-            acc = F(acc + runs[c, tt])
+    g, _ = _level(F(0.0), list(groups), target)
+    acc = pref[g]
+    k, acc = _level(acc, [chunks[c] if c < nch else F(0.0) for c in range(GROUP * g, GROUP * g + GROUP)], target)
+    c = GROUP * g + k
+    t, acc = _level(acc, list(runs[c]), target)
     base = c * CHUNK + t * RUN
-    for e in range(RUN):
-        acc = F(acc + pr[base + e])
-        if acc > target:
-            return base + e
-    return base + max(e for e in range(RUN) if pr[base + e] > 0)
+    e, _ = _level(acc, list(pr[base:base + RUN]), target)
+    return base + e
 
 
 def softmax_parts(row: np.ndarray):
-    """(e = texp(row - max), Z = blocked_sum(e)) for one fp32 row."""
-    mx = np.max(row)
-    e = texp((row - mx).astype(F))
-    return e, blocked_sum(e)
+    """(e, Z) for one fp32 row with per-chunk exponentials: m_c the chunk maxima, M the row's,
+    f_c = texp(m_c - M), e = fl(texp(l - m_c) * f_c) (0 below the smallest normal),
+    Z = group-blocked sum over chunks of fl(f_c * A_c), A_c = blocked chunk total of texp(l - m_c)."""
+    V = row.shape[0]
+    rp = _padded(row, -np.inf).reshape(-1, CHUNK)
+    mc = rp.max(axis=1).astype(F)
+    M = mc.max()
+    a = texp((rp - mc[:, None]).astype(F))
+    f = texp((mc - M).astype(F))
+    e = (a * f[:, None]).astype(F)
+    e = np.where(e < FLT_MIN, F(0.0), e).astype(F).reshape(-1)[:V]
+    _, A = _run_chunk_sums(a)
+    S = (f * A).astype(F)
+    return e, group_parts(S)[1][-1]
 
 
 # ------------------------------------------------------------------ residual rejection sampling
@@ -220,7 +255,7 @@ def residual_accept(logits: np.ndarray, q: np.ndarray, drafts: np.ndarray, u: np
     if R > 0:
         tok = blocked_search(r, F(F(u[K]) * R))
     else:
-        tok = int(np.argmax(p))
+        tok = int(np.argmax(logits[n]))  # the row's first maximum
     return {"n": n, "tok": tok, "pos": pos + n + 1, "slot": n,
             "tokens": [int(t) for t in drafts[:n]] + [tok], "commit": list(range(pos, pos + n + 1))}
 

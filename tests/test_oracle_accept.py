@@ -138,6 +138,27 @@ def test_blocked_sum_and_search_brute_force():
         assert cum[k] >= t - 1e-3 and (k == 0 or cum[k - 1] <= t + 1e-3)
 
 
+def test_softmax_parts_per_chunk_exponentials():
+    """e = fl(texp(l - m_c) texp(m_c - M)) against float64 exp(l - max) (relative 1e-6 where it
+    is normal), Z against the float64 sum of e (1e-6), over rows whose chunks have very
+    different maxima; a one-chunk row is exactly the single-maximum form texp(l - M)."""
+    rng = np.random.default_rng(31)
+    for V in (1000, 5000, 9000):
+        lg = bf16_round((rng.standard_normal(V) * 3).astype(F))
+        lg[: min(V, 1024)] -= F(30.0)                                # a chunk far below the maximum
+        lg = bf16_round(lg)
+        e, Z = a.softmax_parts(lg)
+        ref = np.exp(lg.astype(np.float64) - lg.max())
+        big = ref > 1e-30
+        assert np.all(np.abs(e[big] - ref[big]) <= 1e-6 * ref[big])
+        assert np.all(e[~big] < 1e-29)
+        assert abs(float(Z) - e.astype(np.float64).sum()) <= 1e-6 * float(Z)
+        assert e.argmax() == lg.argmax() and e.max() == F(1.0)
+    one = bf16_round((rng.standard_normal(700) * 3).astype(F))
+    e1, _ = a.softmax_parts(one)
+    assert np.array_equal(e1, a.texp((one - one.max()).astype(F)))
+
+
 def test_residual_p_equals_q_accepts_all():
     lg = _rows(8, 2048, seed=8)
     parts = [a.softmax_parts(lg[i]) for i in range(7)]

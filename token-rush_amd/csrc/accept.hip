@@ -533,8 +533,7 @@ __device__ void merge_lists_top64_thr(const uint32_t* src, int n, uint32_t* out_
 
 // ------------------------------------------------------------------ accept outputs
 
-// FIN_KEYS: the per-chunk keys only (no row reduction; the residual kernels reduce them)
-enum { FIN_NONE = 0, FIN_CHAIN = 1, FIN_TREE = 2, FIN_KEYS = 3 };
+enum { FIN_NONE = 0, FIN_CHAIN = 1, FIN_TREE = 2 };
 
 struct ArgmaxArgs {
   const uint16_t* logits;  // bf16 [M, V]
@@ -543,7 +542,6 @@ struct ArgmaxArgs {
   const int32_t* parent;   // tree: [M]
   uint64_t* keys;          // ws [M * nch]
   int64_t* preds;          // ws [M]
-  float* rowmax;           // ws [M] (row maxima, used by the residual kernels)
   int* cnt_rows;           // ws [M]
   int* cnt_all;            // ws [1]
   AcceptOut o;
@@ -589,7 +587,6 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
     for (int w = 1; w < 4; ++w) best = wmax[w] > best ? wmax[w] : best;
     ws_st(a.keys + blockIdx.x, best);
   }
-  if (a.fin == FIN_KEYS) return;
   if (!arrive_last(a.cnt_rows + row * kCntStride, a.nch)) return;
   if (threadIdx.x < 64) {
     uint64_t b = 0;
@@ -602,7 +599,6 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxArgs a) {
       const int64_t idx = vkey_idx(b);
       if (a.o.pred) a.o.pred[row] = idx;
       ws_st(a.preds + row, idx);
-      if (a.rowmax) ws_st(a.rowmax + row, bf16_bits_to_f32(unord16((uint32_t)(b >> 32))));
     }
   }
   if (!arrive_last(a.cnt_all, a.M)) return;
@@ -720,9 +716,11 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
 
 // ------------------------------------------------------------------ residual rejection sampling
 
-// Phase 1 is argmax_kernel storing its per-chunk keys (FIN_KEYS). Phase 2: the row maxima from
-// those keys; per (row, 1024-chunk) run and chunk sums of e = texp(l - rowmax), e(d_i) and
-// q_i(d_i) kept by the chunk holding draft d_i; per row Z and the row maximum. Phase 3: the
+// Exponentials are taken per 1024-element chunk: with m_c the chunk's maximum and M the row's,
+// a = texp(l - m_c), f_c = texp(m_c - M), e = fl(a f_c) (0 below the smallest normal), and
+// Z = the group-blocked sum of fl(f_c A_c), A_c the chunk's blocked sum of a. So no pass waits
+// for a row maximum. Phase 2: per (row, chunk) m_c and A_c, and a(d_i), q_i(d_i), m_c(d_i)
+// kept by the chunk holding draft d_i; the row's last workgroup takes M and Z. Phase 3: the
 // accept tests u_i q_i(d_i) < e_i(d_i) / Z_i (in every wave), then the draw from row n.
 struct ResidualArgs {
   const uint16_t* logits;  // [K+1, V]
@@ -730,17 +728,41 @@ struct ResidualArgs {
   const int64_t* spec;     // committed + K drafts [K+1]
   const float* u;          // [K+1]
   int M, V, nch;           // M = K + 1 rows, nch = 1024-chunks per row
-  const uint64_t* keys;    // ws [M * nka]: argmax_kernel's per-chunk (value, index) keys
-  int nka;                 // keys per row (<= 64)
-  float* rowmax;           // ws [M]: row maxima, stored by phase 2
-  float* chunk_sum;        // ws [M * nch] (phase 2), then [nch] (phase 3)
+  float* A;                // ws [M * nch]: chunk sums of a (phase 2)
+  float* mc;               // ws [M * nch]: chunk maxima (phase 2)
+  float* chunk_sum;        // ws [nch]: phase 3's chunk sums of r
+  float* rowmax;           // ws [M]
   float* Z;                // ws [M]
-  float* e_draft;          // ws [M]
-  float* q_draft;          // ws [M]: q_i(d_i), stored by the workgroup whose chunk holds d_i
+  float* a_draft;          // ws [M]: a(d_i), q_i(d_i) and m_c(d_i), stored by the chunk holding d_i
+  float* q_draft;
+  float* m_draft;
   int* cnt_rows;
   int* cnt_all;
   AcceptOut o;
 };
+
+constexpr float kFltMin = 1.17549435e-38f;  // smallest normal fp32: products below it count as 0
+
+// Wave maxima of an unsigned key and of a float (DPP / permlane exchanges).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  uint32_t w;
+  w = xor_lane<32>(v); v = w > v ? w : v;
+  w = xor_lane<16>(v); v = w > v ? w : v;
+  w = xor_lane<8>(v); v = w > v ? w : v;
+  w = xor_lane<4>(v); v = w > v ? w : v;
+  w = xor_lane<2>(v); v = w > v ? w : v;
+  w = xor_lane<1>(v); v = w > v ? w : v;
+  return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, __uint_as_float(xor_lane<32>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(xor_lane<16>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(xor_lane<8>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(xor_lane<4>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(xor_lane<2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(xor_lane<1>(__float_as_uint(v))));
+  return v;
+}
 
 // This lane's run (16 elements) of chunk ch of row `row`: logits bits as loaded (two per word,
 // unpacked only where used, so that a load can stay in flight), and q (residual only).
@@ -782,14 +804,19 @@ __device__ __forceinline__ void run_load(const ResidualArgs& a, int row, int ch,
     }
   }
 }
-// The run's values of r from its loaded data: r = e / Z - q clamped at 0 (residual), or e / Z
-// (bonus), or e (phase 2, Z unused). Returns the sequential run sum.
+// The run's values from its loaded data, m = the chunk's maximum and f its factor f_c:
+// r = e / Z - q clamped at 0 (residual), or e / Z (bonus), or a (phase 2; f and Z unused).
+// Returns the sequential run sum.
 template <int MODE>
-__device__ __forceinline__ float r_value(const ResidualArgs& a, int i0, float mx, float Zr, const RunData& d, int e) {
+__device__ __forceinline__ float r_value(const ResidualArgs& a, int i0, float mx, float f, float Zr, const RunData& d, int e) {
   float v = 0.f;
   if (i0 + e < a.V) {
     v = texp(__fsub_rn(bf16_bits_to_f32((d.lw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), mx));
-    if (MODE >= 1) v = __fdiv_rn(v, Zr);
+    if (MODE >= 1) {
+      v = __fmul_rn(v, f);
+      v = v < kFltMin ? 0.f : v;
+      v = __fdiv_rn(v, Zr);
+    }
     if (MODE == 1) {
       v = __fsub_rn(v, d.qv[e]);
       v = v > 0.f ? v : 0.f;
@@ -798,30 +825,42 @@ __device__ __forceinline__ float r_value(const ResidualArgs& a, int i0, float mx
   return v;
 }
 template <int MODE>
-__device__ __forceinline__ float run_finish(const ResidualArgs& a, int ch, int lane, float mx, float Zr, const RunData& d, float (&vals)[kRun]) {
+__device__ __forceinline__ float run_finish(const ResidualArgs& a, int ch, int lane, float mx, float f, float Zr, const RunData& d, float (&vals)[kRun]) {
   const int i0 = ch * kChunk + lane * kRun;
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < kRun; ++e) {
-    vals[e] = r_value<MODE>(a, i0, mx, Zr, d, e);
+    vals[e] = r_value<MODE>(a, i0, mx, f, Zr, d, e);
     s = __fadd_rn(s, vals[e]);
   }
   return s;
 }
 // Elements [E0, E1) of the run's values into out[e * 64 + lane] (element-major: conflict-free).
 template <int MODE, int E0, int E1>
-__device__ __forceinline__ void run_part(const ResidualArgs& a, int row, int ch, int lane, float mx, float Zr, float* out) {
+__device__ __forceinline__ void run_part(const ResidualArgs& a, int row, int ch, int lane, float mx, float f, float Zr, float* out) {
   RunData d;
   run_load<MODE>(a, row, ch, lane, d);
   const int i0 = ch * kChunk + lane * kRun;
 #pragma unroll
-  for (int e = E0; e < E1; ++e) out[e * 64 + lane] = r_value<MODE>(a, i0, mx, Zr, d, e);
+  for (int e = E0; e < E1; ++e) out[e * 64 + lane] = r_value<MODE>(a, i0, mx, f, Zr, d, e);
 }
 template <int MODE>
-__device__ __forceinline__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float Zr, float (&vals)[kRun]) {
+__device__ __forceinline__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float f, float Zr, float (&vals)[kRun]) {
   RunData d;
   run_load<MODE>(a, row, ch, lane, d);
-  return run_finish<MODE>(a, ch, lane, mx, Zr, d, vals);
+  return run_finish<MODE>(a, ch, lane, mx, f, Zr, d, vals);
+}
+
+// A group of 4 chunk values into one lane: lane l gets chunks 4 l .. 4 l + 3 of src (zeros past
+// n; agent-scope loads at clamped addresses, all issued together).
+__device__ __forceinline__ void gather_group(const float* src, int n, float (&g)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = 4 * lane + k;
+    const float v = ws_ld(src + (c < n ? c : n - 1));
+    g[k] = c < n ? v : 0.f;
+  }
 }
 
 // Sum of the 64 lanes' run sums in lane order (every lane gets it).
@@ -865,38 +904,63 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase2_kernel(Residua
   const int ch = (blockIdx.x % nq) * kWavesRes + wave;
   const int K = a.M - 1;
   const int64_t spec_l = lane < K ? a.spec[lane + 1] : -1;  // the finish's drafts, loaded up front
-  // the row maximum from the argmax kernel's chunk keys (one per lane)
-  const uint64_t key = ws_ld(a.keys + (size_t)row * a.nka + (lane < a.nka ? lane : a.nka - 1));
-  const float mx = bf16_bits_to_f32(unord16((uint32_t)(wave_max_u64(key) >> 32)));
   if (ch < a.nch) {
-  float vals[kRun];
-  const float rs = run_values<0>(a, row, ch, lane, mx, 1.f, vals);
-  const float ct = chunk_total(rs);
-  if (row < K) {
-    // the workgroup whose chunk holds draft d keeps e(d) and q(d) for the accept test
-    const int64_t d = __shfl(spec_l, row);
-    const int base = ch * kChunk + lane * kRun;
-    if (d >= base && d < base + kRun) {
-      ws_st(a.e_draft + row, vals[d - base]);
-      ws_st(a.q_draft + row, a.q[(size_t)row * a.V + d]);
+    RunData d;
+    run_load<0>(a, row, ch, lane, d);
+    // the chunk's maximum (ordered bf16 keys of the valid elements, then the wave)
+    const int i0 = ch * kChunk + lane * kRun;
+    uint32_t km = 0;
+#pragma unroll
+    for (int e = 0; e < kRun; ++e) {
+      const uint32_t k = ord16((d.lw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      km = (i0 + e < a.V && k > km) ? k : km;
     }
-  }
-  if (lane == 0) ws_st(a.chunk_sum + (size_t)row * a.nch + ch, ct);
+    const float mc = bf16_bits_to_f32(unord16(wave_max_u32(km)));
+    float vals[kRun];
+    const float rs = run_finish<0>(a, ch, lane, mc, 1.f, 1.f, d, vals);
+    const float ct = chunk_total(rs);
+    if (row < K) {
+      // the wave whose chunk holds draft d keeps a(d), q(d) and the chunk's maximum
+      const int64_t dd = __shfl(spec_l, row);
+      if (dd >= i0 && dd < i0 + kRun) {
+        ws_st(a.a_draft + row, vals[dd - i0]);
+        ws_st(a.q_draft + row, a.q[(size_t)row * a.V + dd]);
+        ws_st(a.m_draft + row, mc);
+      }
+    }
+    if (lane == 0) {
+      ws_st(a.A + (size_t)row * a.nch + ch, ct);
+      ws_st(a.mc + (size_t)row * a.nch + ch, mc);
+    }
   }
   if (!arrive_last(a.cnt_rows + row * kCntStride, nq)) return;
   if (wave) return;
-  float cs[kMaxChunks / 64];
-  gather_chunks(a.chunk_sum + (size_t)row * a.nch, a.nch, cs);
-  const float Zrow = wave_seq_sum(cs);
+  // M, then Z over the groups of 4 chunks (lane l: group l): f_c A_c in chunk order within the
+  // group, then the groups in order
+  float Ag[4], Mg[4];
+  gather_group(a.A + (size_t)row * a.nch, a.nch, Ag);
+  gather_group(a.mc + (size_t)row * a.nch, a.nch, Mg);
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) m = 4 * lane + k < a.nch ? fmaxf(m, Mg[k]) : m;
+  const float M = wave_max_f32(m);
+  float G = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float S = 4 * lane + k < a.nch ? __fmul_rn(texp(__fsub_rn(Mg[k], M)), Ag[k]) : 0.f;
+    G = k == 0 ? S : __fadd_rn(G, S);
+  }
+  const float g1[1] = {G};
+  const float Zrow = wave_seq_sum(g1);
   if (lane == 0) {
     ws_st(a.Z + row, Zrow);
-    ws_st(a.rowmax + row, mx);
+    ws_st(a.rowmax + row, M);
   }
 }
 
 // Phase 3: n from the accept tests, then one row j = n (the first rejected draft's row, or the
 // bonus row K): chunk sums of r, then the last workgroup draws the token with u[K] by a blocked
-// inverse-CDF search.
+// inverse-CDF search (group, chunk, run, element).
 __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(ResidualArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ch = blockIdx.x * kWavesRes + wave;
@@ -906,30 +970,37 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
   // out-of-vocabulary draft fails.
   const int rl = lane < a.M ? lane : 0, dl = lane < K ? lane : 0;
   const float mx_l = ws_ld(a.rowmax + rl), z_l = ws_ld(a.Z + rl);
-  const float e_l = ws_ld(a.e_draft + dl), q_l = ws_ld(a.q_draft + dl), u_l = a.u[dl];
+  const float a_l = ws_ld(a.a_draft + dl), q_l = ws_ld(a.q_draft + dl), md_l = ws_ld(a.m_draft + dl);
+  const float u_l = a.u[dl];
   const int64_t d_l = a.spec[dl + 1];
   const float uK = a.u[K];
-  const bool pass = lane < K && d_l >= 0 && d_l < a.V && __fmul_rn(u_l, q_l) < __fdiv_rn(e_l, z_l);
+  float e_d = __fmul_rn(a_l, texp(__fsub_rn(md_l, mx_l)));
+  e_d = e_d < kFltMin ? 0.f : e_d;
+  const bool pass = lane < K && d_l >= 0 && d_l < a.V && __fmul_rn(u_l, q_l) < __fdiv_rn(e_d, z_l);
   const int j = __builtin_ctzll(~__ballot(pass));  // <= K: lanes from K on do not pass
-  const float mx = lane_val(mx_l, j), Zj = lane_val(z_l, j);
+  const float Mj = lane_val(mx_l, j), Zj = lane_val(z_l, j);
+  const float* mcj = a.mc + (size_t)j * a.nch;
   float vals[kRun];
   if (ch < a.nch) {
-  const float rs = j < K ? run_values<1>(a, j, ch, lane, mx, Zj, vals) : run_values<2>(a, j, ch, lane, mx, Zj, vals);
-  const float ct = chunk_total(rs);
-  if (lane == 0) ws_st(a.chunk_sum + ch, ct);
+    const float mc = ws_ld(mcj + ch);
+    const float f = texp(__fsub_rn(mc, Mj));
+    const float rs = j < K ? run_values<1>(a, j, ch, lane, mc, f, Zj, vals) : run_values<2>(a, j, ch, lane, mc, f, Zj, vals);
+    const float ct = chunk_total(rs);
+    if (lane == 0) ws_st(a.chunk_sum + ch, ct);
   }
   if (!arrive_last(a.cnt_all, gridDim.x)) return;
-  // The last workgroup: wave 0 runs the exact chain over the chunk sums while waves 1-3 compute
+  // The last workgroup: wave 0 runs the exact chain over the group sums while waves 1-3 compute
   // the values of the chunk that an unordered (parallel) scan finds, a third of each run each;
   // the exact search lands on that chunk in all but rounding ties (wave 0 then computes its own).
   __shared__ float sp_vals[kChunk];
   __shared__ int sp_chunk;
-  __shared__ __align__(16) float chain_lds[kMaxChunks];
-  float cs[kMaxChunks / 64];
+  __shared__ __align__(16) float chain_lds[64];
   constexpr int RC = kMaxChunks / 64;
-  float pre[RC];
-  gather_chunks(a.chunk_sum, a.nch, cs);
+  float c4[4], pre1[1], G1[1];
   if (wave) {
+    float cs[RC], ms[RC], pre[RC];
+    gather_chunks(a.chunk_sum, a.nch, cs);
+    gather_chunks(mcj, a.nch, ms);
 #pragma unroll
     for (int k = 0; k < RC; ++k) pre[k] = cs[k];
 #pragma unroll
@@ -950,28 +1021,63 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
     float unused;
     const int c_guess = wave_seq_choose(cs, pre, 0.f, uK * carry, &unused);
     const int cg = c_guess >= 0 ? c_guess : 0;
+    float msel = ms[0];
+#pragma unroll
+    for (int k = 1; k < RC; ++k) msel = (cg >> 6) == k ? ms[k] : msel;
+    const float mg = lane_val(msel, cg & 63), fg = texp(__fsub_rn(mg, Mj));
     if (j < K) {
-      if (wave == 1) run_part<1, 0, 6>(a, j, cg, lane, mx, Zj, sp_vals);
-      else if (wave == 2) run_part<1, 6, 11>(a, j, cg, lane, mx, Zj, sp_vals);
-      else run_part<1, 11, 16>(a, j, cg, lane, mx, Zj, sp_vals);
+      if (wave == 1) run_part<1, 0, 6>(a, j, cg, lane, mg, fg, Zj, sp_vals);
+      else if (wave == 2) run_part<1, 6, 11>(a, j, cg, lane, mg, fg, Zj, sp_vals);
+      else run_part<1, 11, 16>(a, j, cg, lane, mg, fg, Zj, sp_vals);
     } else {
-      if (wave == 1) run_part<2, 0, 6>(a, j, cg, lane, mx, Zj, sp_vals);
-      else if (wave == 2) run_part<2, 6, 11>(a, j, cg, lane, mx, Zj, sp_vals);
-      else run_part<2, 11, 16>(a, j, cg, lane, mx, Zj, sp_vals);
+      if (wave == 1) run_part<2, 0, 6>(a, j, cg, lane, mg, fg, Zj, sp_vals);
+      else if (wave == 2) run_part<2, 6, 11>(a, j, cg, lane, mg, fg, Zj, sp_vals);
+      else run_part<2, 11, 16>(a, j, cg, lane, mg, fg, Zj, sp_vals);
     }
     if (wave == 1 && lane == 0) sp_chunk = cg;
   } else {
-    wave_seq_prefix(cs, 0.f, pre, chain_lds);  // the exact chain: the running sums, the last the total
+    // lane l: group l's chunk sums, its sum in chunk order, then the exact chain over the groups
+    gather_group(a.chunk_sum, a.nch, c4);
+    float G = c4[0];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) G = __fadd_rn(G, c4[k]);
+    G1[0] = G;
+    wave_seq_prefix(G1, 0.f, pre1, chain_lds);  // the running sums, the last the total
   }
   __syncthreads();
   if (wave) return;
-  const float R = lane_val(pre[RC - 1], 63);
+  const float R = lane_val(pre1[0], 63);
   const bool degenerate = !(R > 0.f);
   const float target = __fmul_rn(uK, R);
   int pick = -1;
   if (!degenerate) {
     float acc;
-    const int c = wave_seq_choose(cs, pre, 0.f, target, &acc);
+    const int g = wave_seq_choose(G1, pre1, 0.f, target, &acc);  // the group
+    // its chunk: the first whose running sum from acc exceeds the target, else the last positive
+    float cg4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cg4[k] = lane_val(c4[k], g);
+    int kc = -1;
+    float a0 = acc;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (kc < 0) {
+        const float t = __fadd_rn(a0, cg4[k]);
+        if (t > target) kc = k;
+        else a0 = t;
+      }
+    }
+    if (kc < 0) {
+      int last = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) last = cg4[k] > 0.f ? k : last;
+      kc = last;
+      a0 = acc;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a0 = k < kc ? __fadd_rn(a0, cg4[k]) : a0;
+    }
+    acc = a0;
+    const int c = 4 * g + kc;
     float rs_l = 0.f;
     if (c == sp_chunk) {
 #pragma unroll
@@ -980,7 +1086,8 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
         rs_l = __fadd_rn(rs_l, vals[e]);  // run_finish's sum
       }
     } else {
-      rs_l = j < K ? run_values<1>(a, j, c, lane, mx, Zj, vals) : run_values<2>(a, j, c, lane, mx, Zj, vals);
+      const float mc = ws_ld(mcj + c), f = texp(__fsub_rn(mc, Mj));
+      rs_l = j < K ? run_values<1>(a, j, c, lane, mc, f, Zj, vals) : run_values<2>(a, j, c, lane, mc, f, Zj, vals);
     }
     const float rr[1] = {rs_l};
     float run_acc;
@@ -1084,9 +1191,9 @@ size_t argmax_bytes(int M, int V) { return (size_t)M * nch_arg(V, M) * 8 + (size
 size_t scratch_bytes(int M, int V) {
   const size_t argmax = argmax_bytes(M, V) + (size_t)M * 4;
   const size_t samp = (size_t)M * nch_top(V) * kCand * 8 + (size_t)M * 8;
-  const size_t resid = (size_t)M * nch_run(V) * 4 + (size_t)M * 4 * 4 + 16;
+  const size_t resid = ((size_t)2 * M * nch_run(V) + nch_run(V) + (size_t)5 * M) * 4;
   size_t m = argmax > samp ? argmax : samp;
-  m = m > resid + argmax ? m : resid + argmax;
+  m = m > resid ? m : resid;
   return (m + 255) & ~(size_t)255;
 }
 
@@ -1122,7 +1229,7 @@ AcceptOut make_out(int64_t* pred, int64_t* n, int64_t* tok, int64_t* pos, int64_
 // counters (in units of kCntStride ints): [0, 32) rows of the first kernel, [32] all-rows of
 // the first kernel, [64, 96) rows of the residual phase 2, [128] phase 3.
 int launch_argmax(const void* logits, int M, int V, int fin, const int64_t* spec, const int32_t* parent,
-                  const WsView& w, float* rowmax, const AcceptOut& o, hipStream_t st) {
+                  const WsView& w, const AcceptOut& o, hipStream_t st) {
   ArgmaxArgs a;
   a.logits = (const uint16_t*)logits;
   a.M = M;
@@ -1133,7 +1240,6 @@ int launch_argmax(const void* logits, int M, int V, int fin, const int64_t* spec
   a.parent = parent;
   a.keys = (uint64_t*)w.scratch;
   a.preds = (int64_t*)(w.scratch + (size_t)M * a.nch * 8);
-  a.rowmax = rowmax;
   a.cnt_rows = w.cnt;
   a.cnt_all = w.cnt + 32 * kCntStride;
   a.o = o;
@@ -1157,7 +1263,7 @@ int tr_argmax_rows(const void* logits, int M, int V, void* ws, size_t ws_bytes, 
   WsView w;
   if (!check_mv(M, V)) return TR_ERR_SHAPE;
   if (!logits || !pred || !ws_view(ws, ws_bytes, M, V, &w)) return TR_ERR_ARG;
-  return launch_argmax(logits, M, V, FIN_NONE, nullptr, nullptr, w, nullptr,
+  return launch_argmax(logits, M, V, FIN_NONE, nullptr, nullptr, w,
                        make_out(pred, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr), (hipStream_t)stream);
 }
 
@@ -1169,7 +1275,7 @@ int tr_accept_greedy(const void* logits, int M, int V, const int64_t* spec_toks,
   if (!logits || !spec_toks || !n_accepted || !tok || !pos || !slot || !tokens || !commit ||
       !ws_view(ws, ws_bytes, M, V, &w))
     return TR_ERR_ARG;
-  return launch_argmax(logits, M, V, FIN_CHAIN, spec_toks, nullptr, w, nullptr,
+  return launch_argmax(logits, M, V, FIN_CHAIN, spec_toks, nullptr, w,
                        make_out(pred, n_accepted, tok, pos, slot, tokens, commit), (hipStream_t)stream);
 }
 
@@ -1181,7 +1287,7 @@ int tr_accept_tree(const void* logits, int M, int V, const int64_t* node_toks, c
   if (!logits || !node_toks || !parent || !n_accepted || !tok || !pos || !slot || !tokens || !commit ||
       !ws_view(ws, ws_bytes, M, V, &w))
     return TR_ERR_ARG;
-  return launch_argmax(logits, M, V, FIN_TREE, node_toks, parent, w, nullptr,
+  return launch_argmax(logits, M, V, FIN_TREE, node_toks, parent, w,
                        make_out(pred, n_accepted, tok, pos, slot, tokens, commit), (hipStream_t)stream);
 }
 
@@ -1237,12 +1343,6 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
       !ws_view(ws, ws_bytes, M, V, &w))
     return TR_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
-  // phase 1: the argmax kernel's per-chunk keys (phase 2 reduces them to row maxima)
-  const size_t am = argmax_bytes(M, V);
-  float* rowmax = (float*)(w.scratch + am);
-  int rc = launch_argmax(logits, M, V, FIN_KEYS, nullptr, nullptr, w, nullptr,
-                         make_out(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr), st);
-  if (rc) return rc;
   ResidualArgs a;
   a.logits = (const uint16_t*)logits;
   a.q = q;
@@ -1251,15 +1351,17 @@ int tr_accept_residual(const void* logits, int M, int V, const float* q, const i
   a.M = M;
   a.V = V;
   a.nch = nch_run(V);
-  a.keys = (const uint64_t*)w.scratch;
-  a.nka = nch_arg(V, M);
-  a.rowmax = rowmax;
-  char* r = w.scratch + am + (size_t)M * 4;
-  a.chunk_sum = (float*)r;
-  r += (size_t)M * a.nch * 4;
-  a.Z = (float*)r;
-  a.e_draft = a.Z + M;
-  a.q_draft = a.e_draft + M;
+  // workspace: A and mc [M * nch] each, phase 3's chunk sums [nch], then rowmax, Z, a_draft,
+  // q_draft, m_draft [M] each
+  float* r = (float*)w.scratch;
+  a.A = r;
+  a.mc = a.A + (size_t)M * a.nch;
+  a.chunk_sum = a.mc + (size_t)M * a.nch;
+  a.rowmax = a.chunk_sum + a.nch;
+  a.Z = a.rowmax + M;
+  a.a_draft = a.Z + M;
+  a.q_draft = a.a_draft + M;
+  a.m_draft = a.q_draft + M;
   a.cnt_rows = w.cnt + 64 * kCntStride;
   a.cnt_all = nullptr;  // phase 2 has no all-rows handshake
   a.o = make_out(nullptr, n_accepted, tok, pos, slot, tokens, commit);
