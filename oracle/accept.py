@@ -29,7 +29,7 @@ Fixed arithmetic, shared bit-for-bit with the HIP kernels (token-rush_amd/csrc/a
   * The residual path's exponentials are taken per chunk: with m_c the chunk's maximum and M
     the row's, e = fl(texp(l - m_c) * texp(m_c - M)) (flushed to 0 below the smallest normal),
     and Z sums the chunks as fl(texp(m_c - M) * A_c), A_c the chunk's blocked sum of
-    texp(l - m_c). No pass over the row has to wait for the row maximum.
+    texp(l - m_c). No pass over the row has to wait for the row maximum. p = fl(e * fl(1 / Z)).
 
 Pinning (tests/test_oracle_accept.py): texp against numpy's exp (relative error < 2e-7);
 argmax/top64 against numpy argmax/lexsort; sample against brute-force cases, torch's own
@@ -230,6 +230,11 @@ def softmax_parts(row: np.ndarray):
 
 # ------------------------------------------------------------------ residual rejection sampling
 
+def residual_inv(Z) -> np.float32:
+    """fl(1 / Z): the residual path's probabilities are p = fl(e * fl(1 / Z))."""
+    return F(F(1.0) / F(Z))
+
+
 def residual_accept(logits: np.ndarray, q: np.ndarray, drafts: np.ndarray, u: np.ndarray, pos: int = 0):
     """logits fp32 [K+1, V] (target, temperature 1), q fp32 [K, V] (draft probabilities),
     drafts int64 [K], u fp32 [K+1]. Draft i is accepted when u[i] * q[i, d_i] < p[i, d_i]; at the
@@ -243,13 +248,13 @@ def residual_accept(logits: np.ndarray, q: np.ndarray, drafts: np.ndarray, u: np
     for i in range(K):
         e, Z = parts[i]
         d = int(drafts[i])
-        p_d = F(e[d] / Z)
+        p_d = F(e[d] * residual_inv(Z))
         if F(F(u[i]) * F(q[i, d])) < p_d:
             n += 1
         else:
             break
     e, Z = parts[n]
-    p = (e / Z).astype(F)
+    p = (e * residual_inv(Z)).astype(F)
     r = np.maximum((p - q[n]).astype(F), F(0.0)).astype(F) if n < K else p
     R = blocked_sum(r)
     if R > 0:

@@ -162,7 +162,7 @@ def test_softmax_parts_per_chunk_exponentials():
 def test_residual_p_equals_q_accepts_all():
     lg = _rows(8, 2048, seed=8)
     parts = [a.softmax_parts(lg[i]) for i in range(7)]
-    q = np.stack([(e / Z).astype(F) for e, Z in parts])          # q = the oracle's own p exactly
+    q = np.stack([(e * a.residual_inv(Z)).astype(F) for e, Z in parts])   # q = the oracle's own p exactly
     drafts = np.random.default_rng(9).integers(0, 2048, 7)
     u = np.random.default_rng(10).random(8).astype(F) * F(0.999)
     r = a.residual_accept(lg, q, drafts, u)

@@ -719,7 +719,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
 // Exponentials are taken per 1024-element chunk: with m_c the chunk's maximum and M the row's,
 // a = texp(l - m_c), f_c = texp(m_c - M), e = fl(a f_c) (0 below the smallest normal), and
 // Z = the group-blocked sum of fl(f_c A_c), A_c the chunk's blocked sum of a. So no pass waits
-// for a row maximum. Phase 2: per (row, chunk) m_c and A_c, and a(d_i), q_i(d_i), m_c(d_i)
+// for a row maximum; p = fl(e fl(1 / Z)). Phase 2: per (row, chunk) m_c and A_c, and a(d_i), q_i(d_i), m_c(d_i)
 // kept by the chunk holding draft d_i; the row's last workgroup takes M and Z. Phase 3: the
 // accept tests u_i q_i(d_i) < e_i(d_i) / Z_i (in every wave), then the draw from row n.
 struct ResidualArgs {
@@ -805,17 +805,17 @@ __device__ __forceinline__ void run_load(const ResidualArgs& a, int row, int ch,
   }
 }
 // The run's values from its loaded data, m = the chunk's maximum and f its factor f_c:
-// r = e / Z - q clamped at 0 (residual), or e / Z (bonus), or a (phase 2; f and Z unused).
-// Returns the sequential run sum.
+// r = p - q clamped at 0 (residual), or p (bonus), p = fl(e fl(1 / Z)), or a (phase 2; f and
+// invZ unused). Returns the sequential run sum.
 template <int MODE>
-__device__ __forceinline__ float r_value(const ResidualArgs& a, int i0, float mx, float f, float Zr, const RunData& d, int e) {
+__device__ __forceinline__ float r_value(const ResidualArgs& a, int i0, float mx, float f, float invZ, const RunData& d, int e) {
   float v = 0.f;
   if (i0 + e < a.V) {
     v = texp(__fsub_rn(bf16_bits_to_f32((d.lw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), mx));
     if (MODE >= 1) {
       v = __fmul_rn(v, f);
       v = v < kFltMin ? 0.f : v;
-      v = __fdiv_rn(v, Zr);
+      v = __fmul_rn(v, invZ);
     }
     if (MODE == 1) {
       v = __fsub_rn(v, d.qv[e]);
@@ -825,30 +825,30 @@ __device__ __forceinline__ float r_value(const ResidualArgs& a, int i0, float mx
   return v;
 }
 template <int MODE>
-__device__ __forceinline__ float run_finish(const ResidualArgs& a, int ch, int lane, float mx, float f, float Zr, const RunData& d, float (&vals)[kRun]) {
+__device__ __forceinline__ float run_finish(const ResidualArgs& a, int ch, int lane, float mx, float f, float invZ, const RunData& d, float (&vals)[kRun]) {
   const int i0 = ch * kChunk + lane * kRun;
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < kRun; ++e) {
-    vals[e] = r_value<MODE>(a, i0, mx, f, Zr, d, e);
+    vals[e] = r_value<MODE>(a, i0, mx, f, invZ, d, e);
     s = __fadd_rn(s, vals[e]);
   }
   return s;
 }
 // Elements [E0, E1) of the run's values into out[e * 64 + lane] (element-major: conflict-free).
 template <int MODE, int E0, int E1>
-__device__ __forceinline__ void run_part(const ResidualArgs& a, int row, int ch, int lane, float mx, float f, float Zr, float* out) {
+__device__ __forceinline__ void run_part(const ResidualArgs& a, int row, int ch, int lane, float mx, float f, float invZ, float* out) {
   RunData d;
   run_load<MODE>(a, row, ch, lane, d);
   const int i0 = ch * kChunk + lane * kRun;
 #pragma unroll
-  for (int e = E0; e < E1; ++e) out[e * 64 + lane] = r_value<MODE>(a, i0, mx, f, Zr, d, e);
+  for (int e = E0; e < E1; ++e) out[e * 64 + lane] = r_value<MODE>(a, i0, mx, f, invZ, d, e);
 }
 template <int MODE>
-__device__ __forceinline__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float f, float Zr, float (&vals)[kRun]) {
+__device__ __forceinline__ float run_values(const ResidualArgs& a, int row, int ch, int lane, float mx, float f, float invZ, float (&vals)[kRun]) {
   RunData d;
   run_load<MODE>(a, row, ch, lane, d);
-  return run_finish<MODE>(a, ch, lane, mx, f, Zr, d, vals);
+  return run_finish<MODE>(a, ch, lane, mx, f, invZ, d, vals);
 }
 
 // A group of 4 chunk values into one lane: lane l gets chunks 4 l .. 4 l + 3 of src (zeros past
@@ -976,15 +976,21 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
   const float uK = a.u[K];
   float e_d = __fmul_rn(a_l, texp(__fsub_rn(md_l, mx_l)));
   e_d = e_d < kFltMin ? 0.f : e_d;
-  const bool pass = lane < K && d_l >= 0 && d_l < a.V && __fmul_rn(u_l, q_l) < __fdiv_rn(e_d, z_l);
+  const float iz_l = __fdiv_rn(1.f, z_l);
+  const bool pass = lane < K && d_l >= 0 && d_l < a.V && __fmul_rn(u_l, q_l) < __fmul_rn(e_d, iz_l);
   const int j = __builtin_ctzll(~__ballot(pass));  // <= K: lanes from K on do not pass
-  const float Mj = lane_val(mx_l, j), Zj = lane_val(z_l, j);
+  const float Mj = lane_val(mx_l, j), izj = lane_val(iz_l, j);  // fl(1 / Z_j)
   const float* mcj = a.mc + (size_t)j * a.nch;
   float vals[kRun];
   if (ch < a.nch) {
+    // the run's loads before the chunk maximum's (an agent-scope load, which the compiler
+    // would not let later loads pass)
+    RunData d;
+    if (j < K) run_load<1>(a, j, ch, lane, d);
+    else run_load<2>(a, j, ch, lane, d);
     const float mc = ws_ld(mcj + ch);
     const float f = texp(__fsub_rn(mc, Mj));
-    const float rs = j < K ? run_values<1>(a, j, ch, lane, mc, f, Zj, vals) : run_values<2>(a, j, ch, lane, mc, f, Zj, vals);
+    const float rs = j < K ? run_finish<1>(a, ch, lane, mc, f, izj, d, vals) : run_finish<2>(a, ch, lane, mc, f, izj, d, vals);
     const float ct = chunk_total(rs);
     if (lane == 0) ws_st(a.chunk_sum + ch, ct);
   }
@@ -995,44 +1001,54 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
   __shared__ float sp_vals[kChunk];
   __shared__ int sp_chunk;
   __shared__ __align__(16) float chain_lds[64];
-  constexpr int RC = kMaxChunks / 64;
   float c4[4], pre1[1], G1[1];
   if (wave) {
-    float cs[RC], ms[RC], pre[RC];
-    gather_chunks(a.chunk_sum, a.nch, cs);
-    gather_chunks(mcj, a.nch, ms);
+    // lane l: group l (chunk sums and maxima); an inclusive shuffle scan over the groups, then
+    // the chunk within the chosen group, both in any order
+    float cw[4], mw[4];
+    gather_group(a.chunk_sum, a.nch, cw);
+    gather_group(mcj, a.nch, mw);
+    const float gs = ((cw[0] + cw[1]) + cw[2]) + cw[3];
+    float ps = gs;
 #pragma unroll
-    for (int k = 0; k < RC; ++k) pre[k] = cs[k];
+    for (int o = 1; o < 64; o <<= 1) {
+      const float y = __shfl_up(ps, o);
+      if (lane >= o) ps += y;
+    }
+    const float tgt = uK * lane_val(ps, 63);
+    const unsigned long long over = __ballot(ps > tgt);
+    const unsigned long long pos = __ballot(gs > 0.f);
+    const int gg = over ? __ffsll((long long)over) - 1 : (pos ? 63 - __clzll((long long)pos) : 0);
+    float acc = lane_val(ps, gg) - lane_val(gs, gg);
+    int kk = 3;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {  // the RC scans side by side
+    for (int k = 3; k >= 0; --k) {
+      const float v = lane_val(cw[k], gg);
+      kk = v > 0.f ? k : kk;  // fallback: the first positive chunk of the group
+    }
+    bool found = false;
 #pragma unroll
-      for (int k = 0; k < RC; ++k) {
-        const float y = __shfl_up(pre[k], o);
-        if (lane >= o) pre[k] += y;
+    for (int k = 0; k < 4; ++k) {
+      const float v = lane_val(cw[k], gg);
+      if (!found && acc + v > tgt && v > 0.f) {
+        kk = k;
+        found = true;
       }
+      acc += v;
     }
-    float carry = 0.f;
+    const int cg = 4 * gg + kk;
+    float mg = lane_val(mw[0], gg);
 #pragma unroll
-    for (int k = 0; k < RC; ++k) {
-      const float t = lane_val(pre[k], 63);
-      pre[k] += carry;
-      carry += t;
-    }
-    float unused;
-    const int c_guess = wave_seq_choose(cs, pre, 0.f, uK * carry, &unused);
-    const int cg = c_guess >= 0 ? c_guess : 0;
-    float msel = ms[0];
-#pragma unroll
-    for (int k = 1; k < RC; ++k) msel = (cg >> 6) == k ? ms[k] : msel;
-    const float mg = lane_val(msel, cg & 63), fg = texp(__fsub_rn(mg, Mj));
+    for (int k = 1; k < 4; ++k) mg = kk == k ? lane_val(mw[k], gg) : mg;
+    const float fg = texp(__fsub_rn(mg, Mj));
     if (j < K) {
-      if (wave == 1) run_part<1, 0, 6>(a, j, cg, lane, mg, fg, Zj, sp_vals);
-      else if (wave == 2) run_part<1, 6, 11>(a, j, cg, lane, mg, fg, Zj, sp_vals);
-      else run_part<1, 11, 16>(a, j, cg, lane, mg, fg, Zj, sp_vals);
+      if (wave == 1) run_part<1, 0, 6>(a, j, cg, lane, mg, fg, izj, sp_vals);
+      else if (wave == 2) run_part<1, 6, 11>(a, j, cg, lane, mg, fg, izj, sp_vals);
+      else run_part<1, 11, 16>(a, j, cg, lane, mg, fg, izj, sp_vals);
     } else {
-      if (wave == 1) run_part<2, 0, 6>(a, j, cg, lane, mg, fg, Zj, sp_vals);
-      else if (wave == 2) run_part<2, 6, 11>(a, j, cg, lane, mg, fg, Zj, sp_vals);
-      else run_part<2, 11, 16>(a, j, cg, lane, mg, fg, Zj, sp_vals);
+      if (wave == 1) run_part<2, 0, 6>(a, j, cg, lane, mg, fg, izj, sp_vals);
+      else if (wave == 2) run_part<2, 6, 11>(a, j, cg, lane, mg, fg, izj, sp_vals);
+      else run_part<2, 11, 16>(a, j, cg, lane, mg, fg, izj, sp_vals);
     }
     if (wave == 1 && lane == 0) sp_chunk = cg;
   } else {
@@ -1087,7 +1103,7 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
       }
     } else {
       const float mc = ws_ld(mcj + c), f = texp(__fsub_rn(mc, Mj));
-      rs_l = j < K ? run_values<1>(a, j, c, lane, mc, f, Zj, vals) : run_values<2>(a, j, c, lane, mc, f, Zj, vals);
+      rs_l = j < K ? run_values<1>(a, j, c, lane, mc, f, izj, vals) : run_values<2>(a, j, c, lane, mc, f, izj, vals);
     }
     const float rr[1] = {rs_l};
     float run_acc;
