@@ -149,7 +149,8 @@ int tr_accept_sample(const void* logits, int M, int V, const int64_t* spec_toks,
 
 /* Speculative sampling with residual resample (Leviathan et al. 2023): q fp32 [M-1, V] draft
  * probabilities, u fp32 [M]. Draft i accepted when u[i] q[i, d_i] < p[i, d_i] (p = softmax of
- * row i); at the first rejection j (or j = M-1) tok is drawn with u[M-1] from max(p_j - q_j, 0)
+ * row i in a fixed arithmetic: per-1024-chunk exponentials, blocked sums, p = e fl(1 / Z)); at
+ * the first rejection j (or j = M-1) tok is drawn with u[M-1] from max(p_j - q_j, 0)
  * (p_{M-1} when all pass). No counterpart in the reference (its sampled verify is
  * tr_accept_sample's rule, tokenrush/model.py:302-308; progress.md:649-656). */
 int tr_accept_residual(const void* logits, int M, int V, const float* q, const int64_t* spec_toks,
