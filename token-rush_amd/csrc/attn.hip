@@ -330,16 +330,17 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
       if ((tid & 7) == 0) ksc[fk] = sck;
     }
     {
-      // 4 keys x 8 dims -> 8 rows of V^T (4 keys each): byte e of key i is pv[i] byte e
+      // 4 keys x 8 dims -> 8 rows of V^T (4 keys each): byte e of key i is pv[i] byte e. One
+      // v_perm_b32 gathers byte e of two keys, one scaled conversion (scale 1: exact) makes the
+      // bf16 pair.
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int sh = 8 * (e & 3);
-        uint32_t b[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) b[i] = ((e < 4 ? pv[i].x : pv[i].y) >> sh) & 0xFF;
+        const uint32_t sel = 0x0C0C0000u | ((4u + (e & 3)) << 8) | (uint32_t)(e & 3);  // b0 = lo[e], b1 = hi[e]
+        const uint32_t w01 = __builtin_amdgcn_perm(e < 4 ? pv[1].x : pv[1].y, e < 4 ? pv[0].x : pv[0].y, sel);
+        const uint32_t w23 = __builtin_amdgcn_perm(e < 4 ? pv[3].x : pv[3].y, e < 4 ? pv[2].x : pv[2].y, sel);
         uint2 o;
-        o.x = fp8x2_to_bf16(b[0] | (b[1] << 8), false);
-        o.y = fp8x2_to_bf16(b[2] | (b[3] << 8), false);
+        o.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w01, 1.f, false));
+        o.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w23, 1.f, false));
         *(uint2*)(Vt + (fvd + e) * kVPitch + fv) = o;
       }
       if (tid < kAttnBlk) vsc[tid] = psv;
