@@ -447,7 +447,9 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
       const float kk = ck[t][k0 + j], qq = cq[t][k0 + j];
       S[j].x = S[j].x * eg + kk * dv.x;
       S[j].y = S[j].y * eg + kk * dv.y;
-      *(float2*)(dst + (size_t)(k0 + j) * kGdnV) = S[j];
+      // non-temporal: of the M snapshots only the accepted one is read again (by the next step)
+      __builtin_nontemporal_store(S[j].x, dst + (size_t)(k0 + j) * kGdnV);
+      __builtin_nontemporal_store(S[j].y, dst + (size_t)(k0 + j) * kGdnV + 1);
       o.x += S[j].x * qq;
       o.y += S[j].y * qq;
     }
