@@ -298,16 +298,18 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
   u4 pk0, pk1;
   u2 pv[4];
   float psk, psv;
+  // the cache rows are read once per step: non-temporal, as the GEMM streams its weights
+  constexpr int kNt = 2;
   auto fetch = [&](int blk, bool on) {
     const int key0 = blk * kAttnBlk;
     const int kk = key0 + fk;
-    pk0 = __builtin_amdgcn_raw_buffer_load_b128(krs, on ? kk * kAttnD + fkd : kOob, 0, 0);
-    pk1 = __builtin_amdgcn_raw_buffer_load_b128(krs, on ? kk * kAttnD + fkd + 16 : kOob, 0, 0);
-    psk = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ksr, on ? kk * 4 : kOob, 0, 0));
+    pk0 = __builtin_amdgcn_raw_buffer_load_b128(krs, on ? kk * kAttnD + fkd : kOob, 0, kNt);
+    pk1 = __builtin_amdgcn_raw_buffer_load_b128(krs, on ? kk * kAttnD + fkd + 16 : kOob, 0, kNt);
+    psk = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ksr, on ? kk * 4 : kOob, 0, kNt));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      pv[i] = __builtin_amdgcn_raw_buffer_load_b64(vrs, on ? (key0 + fv + i) * kAttnD + fvd : kOob, 0, 0);
-    psv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vsr, on && tid < kAttnBlk ? (key0 + tid) * 4 : kOob, 0, 0));
+      pv[i] = __builtin_amdgcn_raw_buffer_load_b64(vrs, on ? (key0 + fv + i) * kAttnD + fvd : kOob, 0, kNt);
+    psv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vsr, on && tid < kAttnBlk ? (key0 + tid) * 4 : kOob, 0, kNt));
   };
   fetch(b0, b0 < b1);
   for (int blk = b0; blk < b1; ++blk) {

@@ -345,7 +345,10 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   {
     const float* src = a.rec + slot * a.slot_stride + (size_t)hv * kGdnK * kGdnV + v0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) S[j] = *(const float2*)(src + (size_t)(k0 + j) * kGdnV);
+    for (int j = 0; j < 4; ++j) {  // non-temporal: read once
+      const float* r = src + (size_t)(k0 + j) * kGdnV;
+      S[j] = make_float2(__builtin_nontemporal_load(r), __builtin_nontemporal_load(r + 1));
+    }
   }
   // q / k, v and the gates: every load issued at once (a loop with a runtime bound waited for
   // each iteration's loads); indices past M are clamped to token M - 1 and not stored
