@@ -51,7 +51,8 @@ namespace tr {
 // writes s_memrealtime (100 MHz) at mark i to tr_tl_buf[(b * 16 + w) * kTlMarks + i]. Marks: 0
 // entry, 1 launch constants ready, 2 activations staged, 3 the first two strips issued, 4
 // prologue end (group sums), 5 + r strip r's MACs done (r < 11), 16 a batch's reduction done,
-// 20 exit of the strip loop. The normal build has none of it.
+// 20 exit of the strip loop, 21 the activation loads issued, 22 past the barrier that orders
+// them before the strips. The normal build has none of it.
 #ifdef TR_TIMELINE
 constexpr int kTlMarks = 24, kTlBlocks = 2048;
 __device__ unsigned long long tr_tl_buf[kTlBlocks * 16 * kTlMarks];
@@ -325,7 +326,9 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // Staged kernels: every wave's activation requests enter the CU's in-order memory pipeline
   // before any wave's weight requests, so no wave waits for its activations behind the other
   // waves' strips.
+  TLM(21);
   if constexpr (XDMA) __builtin_amdgcn_s_barrier();
+  TLM(22);
   load_strip<GW>(buf[0], rsrc, active ? strip_off(r0) : oob, lane_off, sm_voff);
   load_strip<GW>(buf[1], rsrc, active ? strip_off(r0 + 1) : oob, lane_off, sm_voff);
   TLM(3);
