@@ -391,10 +391,10 @@ __device__ int lds_append_keys(const uint32_t (&k16)[E], const uint32_t (&idx)[E
 }
 
 // Top-64 of a chunk by a threshold (the fast path of sample_kernel's per-chunk select). tau =
-// the 64th largest of the 256 thread maxima bounds the chunk's 64th largest key from below: the
-// 64 threads whose maxima reach it hold 64 items >= tau. Items >= tau (typically ~75 of 4096 for
-// continuous data) are ranked; more than kTopCap of them (heavy ties, padding) take select_top64
-// instead. Both give the same list: the exact top 64, value descending then index ascending.
+// the 64th largest of the 128 maxima of thread pairs bounds the chunk's 64th largest key from
+// below: the 64 pairs whose maxima reach it hold 64 items >= tau. Items >= tau (typically ~89 of
+// 4096 for continuous data, at most 115 in 2000 simulated chunks) are ranked; more than kTopCap of
+// them (heavy ties, padding) take select_top64 instead. Both give the same list: the exact top 64, value descending then index ascending.
 template <int E>
 __device__ void select_top64_thr(const uint32_t (&k16)[E], const uint32_t (&idx)[E], uint32_t* out_k, uint32_t* out_i) {
   __shared__ uint64_t kk[kTopCap];
@@ -414,7 +414,9 @@ __device__ void select_top64_thr(const uint32_t (&k16)[E], const uint32_t (&idx)
   if (tid == 0) s_cnt = 0;
   __syncthreads();
   if (tid < 64) {
-    const uint32_t mv[4] = {tmax[lane], tmax[64 + lane], tmax[128 + lane], tmax[192 + lane]};
+    // the 64th largest of the 128 maxima of thread pairs (t, t + 128): still 64 items >= it, at
+    // half the ballots of the 256 thread maxima (~89 candidates instead of ~74 for continuous data)
+    const uint32_t mv[2] = {max(tmax[lane], tmax[128 + lane]), max(tmax[64 + lane], tmax[192 + lane])};
     const uint32_t v = wave_kth<kCand>(mv);
     if (lane == 0) s_tau = v;
   }
@@ -485,8 +487,8 @@ __device__ void merge_lists_top64(const uint32_t* src, int n, uint32_t* out_k, u
 }
 
 // The row's top 64 from n <= 64 sorted chunk lists (as merge_lists_top64), by a threshold: tau =
-// the 64th largest of the lists' first four keys bounds the row's 64th largest from below; the
-// entries >= tau (a prefix of each list, typically ~70 in all) are ranked as in
+// the 64th largest of the maxima of pairs of the lists' first four keys bounds the row's 64th
+// largest from below; the entries >= tau (a prefix of each list) are ranked as in
 // select_top64_thr. More than kTopCap of them take merge_lists_top64 instead; both give the same
 // list. Load j of wave w brings list 4 j + w, rank `lane` (one list per load: 4 cache lines,
 // where a list per lane touched 64), all loads issued at once; the lists' first four keys
@@ -518,7 +520,8 @@ __device__ void merge_lists_top64_thr(const uint32_t* src, int n, uint32_t* out_
   }
   __syncthreads();
   if (wid == 0) {
-    const uint32_t head[4] = {heads[lane], heads[64 + lane], heads[128 + lane], heads[192 + lane]};
+    // the 64th largest of the maxima of head pairs: 64 list items >= it (as in select_top64_thr)
+    const uint32_t head[2] = {max(heads[lane], heads[128 + lane]), max(heads[64 + lane], heads[192 + lane])};
     const uint32_t v = wave_kth<kCand>(head);
     if (lane == 0) s_tau = v;
   }
