@@ -101,6 +101,37 @@ def test_sample_inverse_cdf_brute_force():
         assert a.sample(lg, 1.0, 1.0, 64, np.array([uu], F))[0] == want
 
 
+def test_sample_kept_ranks_are_a_prefix():
+    """The top-p / top-k kept set is a prefix of the ranks, so the running sums of the kept p
+    are the running sums of p up to the last kept rank and constant after it, bit for bit (the
+    device kernel takes them from the one pass). Holds because p is sorted descending and
+    fl(c + p) >= c: cum - p never decreases, nor does its rounding. Checked with the oracle's own
+    arithmetic on rows with long flat tails, heavy ties and tiny masses."""
+    rng = np.random.default_rng(11)
+    for trial in range(600):
+        kind = trial % 4
+        if kind == 0:
+            row = rng.standard_normal(4096) * 3
+        elif kind == 1:
+            row = np.round(rng.standard_normal(4096), 1)                  # heavy ties
+        elif kind == 2:
+            row = np.where(rng.random(4096) < 0.01, 30.0, rng.standard_normal(4096))  # a few dominate
+        else:
+            row = rng.standard_normal(4096) * 0.01                         # near-uniform, tiny masses
+        vals, _ = a.top64(bf16_round(row.astype(F)))
+        T = F([0.3, 1.0, 2.5][trial % 3])
+        v = (vals / T).astype(F)
+        e = a.texp((v - v[0]).astype(F))
+        p = (e / np.cumsum(e, dtype=F)[-1]).astype(F)
+        cum = np.cumsum(p, dtype=F)
+        top_p, top_k = [(0.9, 64), (0.5, 40), (1.0, 7), (0.99, 64), (0.05, 64)][trial % 5]
+        keep = ((cum - p).astype(F) < F(top_p)) & (np.arange(a.CANDIDATES) < top_k)
+        n = int(keep.sum())
+        assert n >= 1 and keep[:n].all() and not keep[n:].any()
+        cum2 = np.cumsum(np.where(keep, p, F(0.0)).astype(F), dtype=F)
+        assert np.array_equal(cum2.view(np.uint32), np.where(keep, cum, cum[n - 1]).astype(F).view(np.uint32))
+
+
 def test_verify_chain_planted_prefix():
     rng = np.random.default_rng(6)
     for prefix in range(8):

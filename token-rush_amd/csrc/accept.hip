@@ -655,11 +655,14 @@ __device__ int64_t sample_pick(const uint32_t* tk, const uint32_t* ti, float T, 
   float cum[1];
   wave_seq_prefix(pr, 0.f, cum, cum_s);
   const bool keep = __fsub_rn(cum[0], p) < top_p && i < top_k;
-  const float pk[1] = {keep ? p : 0.f};
-  float cum2[1];
-  wave_seq_prefix(pk, 0.f, cum2, cum_s);
-  const float target = __fmul_rn(u, lane_val(cum2[0], kCand - 1));
-  const float mycum2 = cum2[0];
+  // The kept ranks are a prefix: p is sorted descending and fl(c + p) >= c, so cum - p never
+  // decreases from one rank to the next, nor does its rounding. The running sums of the kept p
+  // are therefore the first running sums bit for bit, and past the last kept rank they stay at
+  // its value (adding zeros): no second sequential pass.
+  const unsigned long long kept = __ballot(keep);
+  const float last = kept ? lane_val(cum[0], 63 - __clzll((long long)kept)) : 0.f;
+  const float target = __fmul_rn(u, last);
+  const float mycum2 = keep ? cum[0] : last;
   const unsigned long long below = __ballot(mycum2 < target);
   int pick = __popcll(below);
   if (pick > kCand - 1) pick = kCand - 1;
