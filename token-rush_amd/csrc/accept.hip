@@ -813,6 +813,19 @@ __device__ __forceinline__ void run_load(const ResidualArgs& a, int row, int ch,
 // The run's values from its loaded data, m = the chunk's maximum and f its factor f_c:
 // r = p - q clamped at 0 (residual), or p (bonus), p = fl(e fl(1 / Z)), or a (phase 2; f and
 // invZ unused). Returns the sequential run sum.
+// The chunk's maximum logit (bf16 value as fp32) from the run's loaded words: the ordered bf16
+// keys of the valid elements, then the wave. Phases 2 and 3 take it from the same words.
+__device__ __forceinline__ float chunk_max(const ResidualArgs& a, int ch, int lane, const RunData& d) {
+  const int i0 = ch * kChunk + lane * kRun;
+  uint32_t km = 0;
+#pragma unroll
+  for (int e = 0; e < kRun; ++e) {
+    const uint32_t k = ord16((d.lw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+    km = (i0 + e < a.V && k > km) ? k : km;
+  }
+  return bf16_bits_to_f32(unord16(wave_max_u32(km)));
+}
+
 template <int MODE>
 __device__ __forceinline__ float r_value(const ResidualArgs& a, int i0, float mx, float f, float invZ, const RunData& d, int e) {
   float v = 0.f;
@@ -913,15 +926,8 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase2_kernel(Residua
   if (ch < a.nch) {
     RunData d;
     run_load<0>(a, row, ch, lane, d);
-    // the chunk's maximum (ordered bf16 keys of the valid elements, then the wave)
     const int i0 = ch * kChunk + lane * kRun;
-    uint32_t km = 0;
-#pragma unroll
-    for (int e = 0; e < kRun; ++e) {
-      const uint32_t k = ord16((d.lw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-      km = (i0 + e < a.V && k > km) ? k : km;
-    }
-    const float mc = bf16_bits_to_f32(unord16(wave_max_u32(km)));
+    const float mc = chunk_max(a, ch, lane, d);
     float vals[kRun];
     const float rs = run_finish<0>(a, ch, lane, mc, 1.f, 1.f, d, vals);
     const float ct = chunk_total(rs);
@@ -989,12 +995,11 @@ __global__ __launch_bounds__(64 * kWavesRes) void residual_phase3_kernel(Residua
   const float* mcj = a.mc + (size_t)j * a.nch;
   float vals[kRun];
   if (ch < a.nch) {
-    // the run's loads before the chunk maximum's (an agent-scope load, which the compiler
-    // would not let later loads pass)
+    // the chunk maximum again from the loaded words (phase 2's value, without a workspace load)
     RunData d;
     if (j < K) run_load<1>(a, j, ch, lane, d);
     else run_load<2>(a, j, ch, lane, d);
-    const float mc = ws_ld(mcj + ch);
+    const float mc = chunk_max(a, ch, lane, d);
     const float f = texp(__fsub_rn(mc, Mj));
     const float rs = j < K ? run_finish<1>(a, ch, lane, mc, f, izj, d, vals) : run_finish<2>(a, ch, lane, mc, f, izj, d, vals);
     const float ct = chunk_total(rs);
