@@ -327,7 +327,7 @@ __device__ __forceinline__ uint32_t wave_kth(const uint32_t (&kv)[R]) {
 }
 
 // The top 64 of n <= kTopCap candidate keys (vkey()s) in LDS, by rank: thread t compares
-// candidate t % kTopCap with one half of the n (rounded up to 8) slots, the halves' counts meet
+// candidate t % kTopCap with one half of the n (rounded up to 32) slots, the halves' counts meet
 // in rank[] (zeroed by the caller), and the candidates of rank < 64 land at their rank. 256
 // threads.
 constexpr int kTopCap = 128;
@@ -336,13 +336,19 @@ __device__ void lds_rank_top64(const uint64_t* kk, int n, int* rank, uint32_t* o
   if (c < n) {
     const uint64_t key = kk[c];
     int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-    const int h = ((n + 7) >> 3) << 2;  // half of n rounded up to 8: 2 h <= kTopCap
+    const int h = ((n + 31) >> 5) << 4;  // half of n rounded up to 32: 2 h <= kTopCap
     const int j0 = half * h;
-    for (int j = 0; j < h; j += 4) {  // slots past n hold 0: below every key
-      r0 += kk[j0 + j] > key;
-      r1 += kk[j0 + j + 1] > key;
-      r2 += kk[j0 + j + 2] > key;
-      r3 += kk[j0 + j + 3] > key;
+    for (int j = 0; j < h; j += 16) {  // slots past n hold 0: below every key
+      uint64_t v[16];  // 16 LDS reads in flight per round trip
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = kk[j0 + j + q];
+#pragma unroll
+      for (int q = 0; q < 16; q += 4) {
+        r0 += v[q] > key;
+        r1 += v[q + 1] > key;
+        r2 += v[q + 2] > key;
+        r3 += v[q + 3] > key;
+      }
     }
     atomicAdd(&rank[c], (r0 + r1) + (r2 + r3));
   }
