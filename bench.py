@@ -267,28 +267,64 @@ def config4_tree_step(torch, dev, model, reps=10, M=32):
     """benchmark config 4 through the config-5 model: a seeded 32-node draft tree (branching <= 4,
     depth <= 7) verified by the 64-layer step with the tree mixers (ancestor-masked attention,
     per-node GDN states), M = 32 GEMMs, lm_head, tree accept and commit (KV rows, scales, conv
-    rings), one hipGraph (VerifyModel.step_tree)."""
+    rings), one hipGraph (VerifyModel.step_tree). The node tokens are planted from a first eager
+    pass so that the deepest root path is accepted (its nodes hold their parents' argmax, every
+    other node a different token): each timed replay then commits a real path. Each replay starts
+    from the same restored decode state and is timed alone with HIP events on the launch stream."""
+    import numpy as np
     from tokenrush_amd.accept import AcceptState
     from tokenrush_amd.step import prepare
     prepare(model, M)
     gen = torch.Generator(device=dev)
     gen.manual_seed(8)
     x0 = torch.randn(M, model.cfg.hidden, device=dev, generator=gen).to(torch.bfloat16)
-    toks = torch.randint(0, model.cfg.vocab, (M,), device=dev, generator=gen)
-    parent = torch.tensor(_random_parent(M, seed=4), dtype=torch.int32, device=dev)
+    parent_l = _random_parent(M, seed=4)
+    parent = torch.tensor(parent_l, dtype=torch.int32, device=dev)
     st = AcceptState(M, dev)
-    st.pos.fill_(model.cfg.live)
-    st.slot.zero_()
+    snap = model.state.snapshot()
+
+    def reset():
+        model.state.restore(snap)
+        st.pos.fill_(model.cfg.live)
+        st.slot.zero_()
+
+    reset()
+    pred = model.lm_head(model.hidden(x0, st.pos, st.slot, parent)).float().argmax(-1).cpu().numpy()
+    depth = [0] * M
+    for i in range(1, M):
+        depth[i] = depth[parent_l[i]] + 1
+    node, path = int(np.argmax(depth)), []
+    while node >= 0:
+        path.append(node)
+        node = parent_l[node]
+    V = model.cfg.vocab
+    toks_l = [7] + [(int(pred[parent_l[i]]) + 1) % V for i in range(1, M)]
+    for i in path[:-1]:
+        toks_l[i] = int(pred[parent_l[i]])
+    toks = torch.tensor(toks_l, dtype=torch.int64, device=dev)
+    reset()
     g = graph_of(torch, lambda: model.step_tree(x0, toks, parent, st))
-    # each replay advances pos by the accepted depth + 1 <= 8
-    assert (reps + 3) * 8 <= model.cfg.headroom
-    st.pos.fill_(model.cfg.live)
-    t = timed_graph(torch, g, reps=reps)
-    del g
+    times, accepted = [], []
+    stream = torch.cuda.current_stream()
+    for _ in range(reps + 1):
+        reset()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e-3)
+        accepted.append(int(st.n_accepted))
+    times, accepted = times[1:], accepted[1:]          # the first replay warms up
+    del g, snap
+    t = sum(times) / len(times)
     return {"ms_per_step": round(t * 1e3, 3), "M": M, "replays": reps,
+            "accepted_depth": sorted(set(accepted)), "planted_depth": len(path) - 1,
             "note": "one hipGraph: 257 int4 GEMMs at M=32, tree GDN steps (per-node state, 32 snapshot slots), "
                     "ancestor-masked FP8 attention over 8192 live tokens, lm_head 248320x5120 writing logits, tree "
-                    "accept, commit of KV rows/scales (4 launches) and conv rings (1 launch)"}
+                    "accept, commit of KV rows/scales (4 launches) and conv rings (1 launch); node tokens planted "
+                    "along the deepest root path, each replay from the same restored state"}
 
 
 TL_MARKS = {0: "entry", 1: "launch constants", 21: "activation loads issued", 22: "past the ordering barrier",

@@ -205,6 +205,12 @@ int tr_add_rmsnorm(const void* x, const void* h, int h_mode, int n_slots, const 
  * Replaces: silu_mul (tokenrush/fused.py:67-87). */
 int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* stream);
 
+/* Embedding gather: out [T, H] bf16 = table[ids[t]] for int64 ids [T] (device) over a bf16 table
+ * [V, H]. H % 8 == 0, pointers 16-byte aligned. An id outside [0, V) gives a zero row and sets
+ * *status = 1 when status is not null.
+ * Replaces: x = self.w.embed[tokens] (tokenrush/model.py:215), inside the verify step's graph. */
+int tr_embed_rows(const void* table, const int64_t* ids, void* out, int T, int H, long V, int* status, void* stream);
+
 /* ---------------------------------------------------------------- GDN (gated delta rule) step */
 
 /* Bytes of the workspace tr_gdn_step / tr_gdn_tree_step need for M tokens (up to 32), H key heads and HV value heads (0 if

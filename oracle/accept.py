@@ -235,28 +235,35 @@ def residual_inv(Z) -> np.float32:
     return F(F(1.0) / F(Z))
 
 
-def residual_accept(logits: np.ndarray, q: np.ndarray, drafts: np.ndarray, u: np.ndarray, pos: int = 0):
+def residual_accept(logits: np.ndarray, q: np.ndarray, drafts: np.ndarray, u: np.ndarray, pos: int = 0,
+                    cache: dict = None):
     """logits fp32 [K+1, V] (target, temperature 1), q fp32 [K, V] (draft probabilities),
     drafts int64 [K], u fp32 [K+1]. Draft i is accepted when u[i] * q[i, d_i] < p[i, d_i]; at the
     first rejection j (or j = K when all pass) one token is drawn with u[K] by inverse CDF from
-    max(p[j] - q[j], 0) (from p[K] when j = K). Returns dict like verify_chain plus 'pick'."""
+    max(p[j] - q[j], 0) (from p[K] when j = K). Returns dict like verify_chain plus 'pick'.
+    cache: a dict kept by the caller across calls with the same logits and q (many drafts and
+    uniforms); it holds each row's p and residual so they are computed once."""
     K = drafts.shape[0]
+    cache = {} if cache is None else cache
+
+    def prob(i):
+        if ("p", i) not in cache:
+            e, Z = softmax_parts(logits[i])
+            cache[("p", i)] = (e * residual_inv(Z)).astype(F)
+        return cache[("p", i)]
+
     n = 0
-    parts = []
-    for i in range(K + 1):
-        parts.append(softmax_parts(logits[i]))
     for i in range(K):
-        e, Z = parts[i]
         d = int(drafts[i])
-        p_d = F(e[d] * residual_inv(Z))
-        if F(F(u[i]) * F(q[i, d])) < p_d:
+        if F(F(u[i]) * F(q[i, d])) < prob(i)[d]:
             n += 1
         else:
             break
-    e, Z = parts[n]
-    p = (e * residual_inv(Z)).astype(F)
-    r = np.maximum((p - q[n]).astype(F), F(0.0)).astype(F) if n < K else p
-    R = blocked_sum(r)
+    if ("r", n) not in cache:
+        p = prob(n)
+        r = np.maximum((p - q[n]).astype(F), F(0.0)).astype(F) if n < K else p
+        cache[("r", n)] = (r, blocked_sum(r))
+    r, R = cache[("r", n)]
     if R > 0:
         tok = blocked_search(r, F(F(u[K]) * R))
     else:
@@ -332,3 +339,14 @@ def random_tree(n: int, seed: int, max_branch: int = 4, max_depth: int = 7) -> n
         depth[i] = depth[j] + 1
         kids[j] += 1
     return parent
+
+
+def deep_branch_tree(n: int = 32) -> np.ndarray:
+    """parent int32 [n] whose branch nodes sit deep: a chain 0..10, then nodes off depths 8, 9,
+    10 and below (node 9, depth 9, has four children; node 12, depth 10, two), and the rest
+    hung off the deepest chain. Exercises trees whose branch parents are deeper than a kernel's
+    fixed state stack."""
+    par = [-1] + list(range(10)) + [9, 9, 10, 12, 12, 14, 11, 15, 9, 13, 20, 17, 8]
+    while len(par) < n:
+        par.append(len(par) - 1)
+    return np.array(par[:n], dtype=np.int32)

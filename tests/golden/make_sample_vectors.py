@@ -16,6 +16,7 @@ REF = "/root/reference"
 
 
 def main():
+    sys.dont_write_bytecode = True  # the reference tree is read-only: no __pycache__ there
     sys.path.insert(0, REF)
     from tokenrush.sample import SamplingParams, sample    # the reference's module (imports torch only)
     torch.set_num_threads(8)

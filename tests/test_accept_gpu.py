@@ -174,6 +174,37 @@ def test_accept_residual_config3(dev, seed):
     check_state(st, ref, 8)
 
 
+def test_accept_residual_config3_drafts_from_q(dev):
+    """240 draws at the full vocabulary (V = 248320): q a perturbed copy of the target's own
+    distribution, drafts drawn from q, uniforms drawn fresh, so acceptance, rejection near the
+    u q < p boundary and the residual resample all run at full width (every accepted length
+    0..7 occurs)."""
+    from tokenrush_amd.accept import accept_residual
+    say("residual config 3, drafts drawn from q")
+    K, V = 7, V_FULL
+    rng = np.random.default_rng(77)
+    lg = oa.planted_logits(K + 1, V, seed=78)
+    z = lg[:K].astype(np.float64) + rng.standard_normal((K, V)) * 0.7
+    e = np.exp(z - z.max(-1, keepdims=True))
+    q = (e / e.sum(-1, keepdims=True)).astype(F)
+    cdf = np.cumsum(q.astype(np.float64), -1)
+    x, qd = dev_logits(lg), torch.from_numpy(q).to(dev)
+    cache, seen = {}, set()
+    st = state(8, pos=0)
+    for trial in range(240):
+        spec = np.zeros(K + 1, np.int64)
+        spec[0] = trial
+        spec[1:] = [min(int(np.searchsorted(cdf[i], rng.random() * cdf[i, -1])), V - 1) for i in range(K)]
+        u = rng.random(K + 1).astype(F)
+        st.pos.fill_(trial)
+        st.slot.fill_(0)
+        accept_residual(x, qd, torch.from_numpy(spec).to(dev), torch.from_numpy(u).to(dev), st)
+        ref = oa.residual_accept(lg, q, spec[1:], u, pos=trial, cache=cache)
+        check_state(st, ref, 8)
+        seen.add(ref["n"])
+    assert seen == set(range(K + 1)), seen
+
+
 def test_accept_residual_small_vocab_many_draws(dev):
     """Many draws on a small vocabulary (bonus row, residual rows, p == q edge) against the oracle."""
     from tokenrush_amd.accept import accept_residual

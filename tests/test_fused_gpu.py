@@ -75,3 +75,27 @@ def test_silu_mul_strided_slice(dev):
     wide = _bf(rng, 8, 16384, std=2.0)
     got = silu_mul(_dev(wide)[:, :12288])
     _ulp_close(got, f.silu_mul(wide[:, :12288]))
+
+
+@pytest.mark.parametrize("T,H", [(8, 5120), (1, 1000), (32, 64)])
+def test_embed_rows(dev, T, H):
+    """tr_embed_rows equals the table's rows at the ids bit for bit (model.py:215); an id outside
+    the vocabulary gives a zero row and raises the status word."""
+    from tokenrush_amd.fused import embed_rows
+    print(f"embed_rows T={T} H={H}", flush=True)
+    rng = np.random.default_rng(T + H)
+    V = 3001
+    table = _bf(rng, V, H)
+    ids = rng.integers(0, V, T).astype(np.int64)
+    ids[0] = V - 1
+    status = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    got = embed_rows(_dev(table), torch.from_numpy(ids).to("cuda:0"), status=status)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.float().cpu().numpy(), table[ids]) and int(status) == 0
+    bad = ids.copy()
+    bad[-1] = V
+    got = embed_rows(_dev(table), torch.from_numpy(bad).to("cuda:0"), status=status)
+    torch.cuda.synchronize()
+    assert int(status) == 1
+    assert np.array_equal(got.float().cpu().numpy()[:-1], table[ids[:-1]])
+    assert not got[-1].float().abs().sum().item()

@@ -94,6 +94,9 @@ def test_strips_per_workgroup_agree(dev, R, M):
     torch.cuda.synchronize()
     check_close(y, o.gemm_exact(x, p, s, m), f"R={R}")
     assert torch.equal(y, gfx950.mul(dev_x(x), B, sp, mp))
+    if R == 1 and M == 8:
+        # marlin.mul's positional thread_k, thread_n, sms (marlin.py:138) are accepted and ignored
+        assert torch.equal(gfx950.mul(dev_x(x), B, sp, mp, 64, 256, 16), y)
 
 
 @pytest.mark.parametrize("slots", [2, 3, 5, 12])

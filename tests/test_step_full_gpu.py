@@ -237,3 +237,68 @@ def test_full_size_residual_step_in_one_graph(full_model):
     _check_accept(st, want)
     eager = [t.clone() for t in (lg, st.n_accepted, st.tok, st.pos, st.slot, st.tokens, st.commit)]
     _capture_and_replay(m, reset_state, lambda: m.step(x0, spec, st, q=q, u=u), st, eager, x0)
+
+
+def test_full_size_verify_from_token_ids_in_one_graph(full_model):
+    """The reference's _verify_step whole (model.py:293-312): token ids embedded on the device
+    (model.py:215), body, lm_head, greedy accept, with spec_logits[:M] and spec_hidden[:M] kept
+    (model.py:300-301). Eager verify() equals step() on torch's embedding rows bit for bit; the
+    captured graph reproduces spec_x, spec_hidden, spec_logits and the accept over replays."""
+    from tokenrush_amd.accept import AcceptState
+    m = full_model
+    print("config-5 verify from token ids", flush=True)
+    g = torch.Generator(device="cuda:0").manual_seed(14)
+    st, live, V = AcceptState(M, "cuda:0"), m.cfg.live, m.cfg.vocab
+    spec = torch.randint(0, V, (M,), device="cuda:0", generator=g)
+
+    def reset():
+        m.state.restore(m.initial_state)
+        st.pos.fill_(live)
+        st.slot.zero_()
+
+    reset()
+    pred = m.body(m.embed[spec]).float().argmax(-1)
+    spec[1:4] = pred[0:3]                              # 3 drafts the target agrees with
+    spec[4:] = (pred[3:7] + 1) % V
+    reset()
+    lg_ref = m.step(m.embed[spec].contiguous(), spec, st).clone()
+    hid_ref = m.spec_hidden[:M].clone()
+    acc_ref = [t.clone() for t in (st.n_accepted, st.tok, st.pos, st.slot, st.tokens, st.commit)]
+    assert int(st.n_accepted) == 3
+    reset()
+    m.embed_status.zero_()
+    lg = m.verify(spec, st)
+    torch.cuda.synchronize()
+    assert int(m.embed_status) == 0
+    assert torch.equal(m.spec_x[:M], m.embed[spec])
+    assert torch.equal(lg, lg_ref) and torch.equal(m.spec_logits[:M], lg_ref)
+    assert torch.equal(m.spec_hidden[:M], hid_ref)
+    for a, b in zip((st.n_accepted, st.tok, st.pos, st.slot, st.tokens, st.commit), acc_ref):
+        assert torch.equal(a, b)
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        reset()
+        m.verify(spec, st)                             # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        m.verify(spec, st)
+    for rep in range(2):
+        reset()
+        m.spec_hidden.zero_()
+        m.spec_logits.zero_()
+        m.spec_x.zero_()
+        st.n_accepted.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m.spec_x[:M], m.embed[spec]), rep
+        assert torch.equal(m.spec_hidden[:M], hid_ref), rep
+        assert torch.equal(m.spec_logits[:M], lg_ref), rep
+        for a, b in zip((st.n_accepted, st.tok, st.pos, st.slot, st.tokens, st.commit), acc_ref):
+            assert torch.equal(a, b), rep
+        _ = m.body(m.embed[spec])                      # eager work between replays
+        torch.cuda.synchronize()
+    del graph

@@ -50,6 +50,8 @@ def _tree(kind, M, seed):
         p = np.zeros(M, np.int32)
         p[0] = -1
         return p
+    if kind == "deep":
+        return oa.deep_branch_tree(M)
     return oa.random_tree(M, seed)
 
 
@@ -83,7 +85,7 @@ def _gdn_tree(w, qkvz, x, ring, rec, slot, pos, parent_np, dev):
 
 
 @pytest.mark.parametrize("kind,M,pos,slot", [("random", 32, 1000, 5), ("random", 17, 2, 31), ("star", 9, 40, 0),
-                                             ("chain", 32, 77, 3)])
+                                             ("chain", 32, 77, 3), ("deep", 32, 500, 6), ("deep", 24, 3, 30)])
 def test_gdn_tree_matches_oracle(dev, kind, M, pos, slot):
     print(f"gdn tree {kind} M={M} pos={pos} slot={slot}", flush=True)
     parent = _tree(kind, M, 100 + M)

@@ -9,6 +9,8 @@
 // One workgroup per row, 8 elements per thread in registers between the two passes; N % 8 == 0,
 // N <= 8192, at most 8 partial slots.
 //
+// embed_rows (tokenrush/model.py:215, x = embed[tokens]): out[t] = table[ids[t]], bf16 rows.
+//
 // silu_mul (tokenrush/fused.py:67-87): y[t, i] = silu(gate[t, i]) * up[t, i] with gate_up[t] =
 // [gate (F) | up (F)] (rows ld elements apart), fp32 arithmetic, bf16 out.
 #include "tr_common.h"
@@ -107,6 +109,20 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   *(uint4*)(y + (size_t)t * F + i0) = pack8(out);
 }
 
+// One 16-byte vector per thread; grid (row chunks, T). An id outside [0, V) writes a zero row and
+// sets *status to 1 (the reference's indexing would raise; a device kernel can only report).
+__global__ void embed_rows_kernel(const uint16_t* __restrict__ table, const int64_t* __restrict__ ids,
+                                  uint16_t* __restrict__ out, int H, long V, int* status) {
+  const int t = blockIdx.y;
+  const int i = (blockIdx.x * blockDim.x + threadIdx.x) * kRowVec;
+  if (i >= H) return;
+  const int64_t id = ids[t];
+  const bool ok = id >= 0 && id < V;
+  const uint4 v = ok ? *(const uint4*)(table + (size_t)id * H + i) : make_uint4(0u, 0u, 0u, 0u);
+  *(uint4*)(out + (size_t)t * H + i) = v;
+  if (!ok && i == 0 && status) *status = 1;
+}
+
 }  // namespace tr
 
 using namespace tr;
@@ -147,6 +163,17 @@ int tr_add_rmsnorm(const void* x, const void* h, int h_mode, int n_slots, const 
     }
   }
   return e == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+}
+
+int tr_embed_rows(const void* table, const int64_t* ids, void* out, int T, int H, long V, int* status,
+                  void* stream) {
+  if (!table || !ids || !out) return TR_ERR_ARG;
+  if (T < 0 || H <= 0 || H % kRowVec || V <= 0) return TR_ERR_SHAPE;
+  if (T == 0) return TR_OK;
+  const int per_block = 256 * kRowVec;
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((H + per_block - 1) / per_block, T), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)table, ids, (uint16_t*)out, H, V, status);
+  return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
 }
 
 int tr_silu_mul(const void* gate_up, long ld, void* y, int T, int F, void* stream) {

@@ -50,6 +50,7 @@ SIGNATURES = {
     "tr_commit_rows": (_I, [_P, _I, ctypes.c_long, _I, _P, _P, _P, _I, _P, _P]),
     "tr_add_rmsnorm": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _I, ctypes.c_float, _I, _P]),
     "tr_silu_mul": (_I, [_P, ctypes.c_long, _P, _I, _I, _P]),
+    "tr_embed_rows": (_I, [_P, _P, _P, _I, _I, ctypes.c_long, _P, _P]),
     "tr_gdn_workspace_bytes": (_S, [_I, _I, _I]),
     "tr_attn_workspace_bytes": (_S, [_I, _I, _I]),
     "tr_attn_prep": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, ctypes.c_float, _P]),

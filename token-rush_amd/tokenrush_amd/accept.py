@@ -142,12 +142,13 @@ _lm_ws = {}
 
 
 def lm_head_greedy(lm_head, hidden: torch.Tensor, spec_toks: torch.Tensor, st: AcceptState,
-                   keep_logits: bool = False):
+                   keep_logits: bool = False, out: torch.Tensor = None):
     """logits = lm_head(hidden) and the greedy verify accept in one launch (the GEMM's epilogue
     keeps each row's argmax; the last workgroup finishes the accept exactly as accept_greedy
     does). lm_head: a gfx950 QLinear [V, K]; hidden [M, K] bf16. Returns the logits [M, V] when
     keep_logits (the reference keeps them, model.py:300), else None -- then they are never
-    written. spec_toks None: only st.pred is written (argmax per row). Shapes whose plan splits K
+    written; out (contiguous bf16 [M, V]) receives them instead of a new tensor. spec_toks None:
+    only st.pred is written (argmax per row). Shapes whose plan splits K
     across workgroups (M > 16 at K = 5120) run the product and then the accept kernel."""
     from . import gfx950
     if lm_head.backend != "gfx950" or lm_head.layout != "rows":
@@ -158,8 +159,10 @@ def lm_head_greedy(lm_head, hidden: torch.Tensor, spec_toks: torch.Tensor, st: A
     if hidden.dtype != torch.bfloat16 or K != lm_head.shape[1] or st.M < M:
         raise RuntimeError("lm_head_greedy: hidden must be bf16 [M, K] matching the weight")
     need = int(_lib.lib().tr_lm_head_workspace_bytes(V, K, M))
+    if out is not None and (out.dtype != torch.bfloat16 or tuple(out.shape) != (M, V) or not out.is_contiguous()):
+        raise RuntimeError(f"lm_head_greedy: out must be contiguous bf16 [{M}, {V}]")
     if need == 0:                  # more than one K slot: the product, then the accept kernel
-        logits = lm_head(hidden)
+        logits = lm_head(hidden, out=out)
         if spec_toks is None:
             _lib.check(_lib.lib().tr_argmax_rows(_lib.ptr(logits), M, V, _lib.ptr(workspace(M, V, hidden.device)),
                                                  workspace(M, V, hidden.device).numel(), _lib.ptr(st.pred),
@@ -169,7 +172,8 @@ def lm_head_greedy(lm_head, hidden: torch.Tensor, spec_toks: torch.Tensor, st: A
         return logits if keep_logits else None
     key = hidden.device.index or 0
     ws = _lib.grown_workspace(_lm_ws, key, need, hidden.device)
-    logits = torch.empty(M, V, dtype=torch.bfloat16, device=hidden.device) if keep_logits else None
+    logits = (out if out is not None else torch.empty(M, V, dtype=torch.bfloat16, device=hidden.device)) \
+        if keep_logits or out is not None else None
     spec = None if spec_toks is None else spec_toks[:M].to(torch.long).contiguous()
     x = hidden.contiguous()
     P = _lib.ptr

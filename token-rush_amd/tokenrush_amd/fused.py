@@ -12,16 +12,18 @@ from . import _lib
 H_NONE, H_BF16, H_PARTIALS = 0, 1, 2
 
 
-def add_rmsnorm(x: torch.Tensor, h, weight: torch.Tensor, eps: float, plain: bool = False):
+def add_rmsnorm(x: torch.Tensor, h, weight: torch.Tensor, eps: float, plain: bool = False, out: torch.Tensor = None):
     """x [T, N] bf16; h None, [T, N] bf16 or [S, T, N] fp32 partials -> (x + h as bf16,
     rmsnorm(x + h)); with h None -> (x, rmsnorm(x)). plain: weight * x gain instead of
-    (1 + weight) (fused.py:50-60)."""
+    (1 + weight) (fused.py:50-60). out (contiguous bf16 [T, N]) receives the norm."""
     _lib.require_gpu(x, weight)
     if x.dtype != torch.bfloat16 or x.dim() != 2 or weight.dtype != torch.bfloat16:
         raise RuntimeError("add_rmsnorm: x must be bf16 [T, N] and weight bf16 [N]")
     T, N = x.shape
     x = x.contiguous()
-    y = torch.empty_like(x)
+    if out is not None and (out.dtype != torch.bfloat16 or out.shape != x.shape or not out.is_contiguous()):
+        raise RuntimeError("add_rmsnorm: out must be contiguous bf16 [T, N]")
+    y = torch.empty_like(x) if out is None else out
     if h is None:
         mode, S, hp, xo = H_NONE, 1, None, x
     elif h.dim() == 2:
@@ -52,3 +54,23 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     _lib.check(_lib.lib().tr_silu_mul(_lib.ptr(gate_up), gate_up.stride(0) if T > 1 else F2, _lib.ptr(y), T, F2 // 2,
                                       _lib.stream_of(gate_up)), "tr_silu_mul")
     return y
+
+
+def embed_rows(table: torch.Tensor, ids: torch.Tensor, out: torch.Tensor = None, status: torch.Tensor = None):
+    """table [V, H] bf16, ids int64 [T] on the device -> table[ids] [T, H] bf16, one launch
+    (the reference's x = embed[tokens], model.py:215). An id outside [0, V) gives a zero row and
+    sets status (int32 [1], optional) to 1."""
+    _lib.require_gpu(table, ids)
+    if table.dtype != torch.bfloat16 or table.dim() != 2 or ids.dtype != torch.int64 or ids.dim() != 1:
+        raise RuntimeError("embed_rows: table must be bf16 [V, H] and ids int64 [T]")
+    V, H = table.shape
+    T = ids.shape[0]
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=table.device)
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (T, H) or not out.is_contiguous():
+        raise RuntimeError("embed_rows: out must be contiguous bf16 [T, H]")
+    if status is not None and (status.dtype != torch.int32 or not status.is_cuda):
+        raise RuntimeError("embed_rows: status must be a device int32 tensor")
+    _lib.check(_lib.lib().tr_embed_rows(_lib.ptr(table.contiguous()), _lib.ptr(ids.contiguous()), _lib.ptr(out), T, H,
+                                        V, _lib.ptr(status), _lib.stream_of(table)), "tr_embed_rows")
+    return out

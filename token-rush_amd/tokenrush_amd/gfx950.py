@@ -162,11 +162,18 @@ def _launch(x, B, s, y, partial, n_slots, strips_per_wg=-1, slots=0):
     _lib.check(rc, f"tr_int4_gemm (m={M}, n={N}, k={K})")
 
 
-def mul(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor = None, strips_per_wg=-1, slots=0):
+def mul(x: torch.Tensor, B: torch.Tensor, s: torch.Tensor, m: torch.Tensor = None, thread_k=-1, thread_n=-1, sms=-1,
+        *, strips_per_wg=-1, slots=0, out: torch.Tensor = None):
     """x [M, K] bf16 (M <= 32) -> [M, N] bf16 (marlin.mul, marlin.py:138-145).
-    s (from pack) supplies the scale dtype; m is accepted for call compatibility.
-    strips_per_wg / slots override the tiling (0 / -1 = default)."""
-    y = torch.empty(x.shape[0], B.shape[0] * 16, dtype=torch.bfloat16, device=x.device)
+    s (from pack) supplies the scale dtype; m is accepted for call compatibility. thread_k,
+    thread_n and sms sit where marlin.mul has them and are ignored (this kernel picks its own
+    tiling). strips_per_wg / slots (keyword-only) override the tiling (-1 / 0 = default); out, a
+    contiguous bf16 [M, N] tensor, receives the product instead of a new one."""
+    del thread_k, thread_n, sms
+    shape = (x.shape[0], B.shape[0] * 16)
+    if out is not None and (out.dtype != torch.bfloat16 or tuple(out.shape) != shape or not out.is_contiguous()):
+        raise RuntimeError(f"mul: out must be contiguous bf16 {list(shape)}")
+    y = torch.empty(*shape, dtype=torch.bfloat16, device=x.device) if out is None else out
     _launch(x, B, s, y, False, 0, strips_per_wg, slots)
     return y
 

@@ -106,12 +106,16 @@ class QLinear:
     def dequantize(self) -> torch.Tensor:
         return dequantize_int4(*self.nibbles())
 
-    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+    def __call__(self, x: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+        """x [T, K] -> [T, N]; out (bf16 [T, N], contiguous) receives the product when given."""
         T = x.shape[0]
         if self.backend == "dequant" or T > MAX_ROWS:
-            return F.linear(x, self.dequantize().to(x.dtype))
-        y = gfx950.mul(x.contiguous(), self.B, self.s)
-        return gfx950.unpair(y) if self.layout == "gate_up" else y
+            y = F.linear(x, self.dequantize().to(x.dtype))
+        elif self.layout == "gate_up":
+            y = gfx950.unpair(gfx950.mul(x.contiguous(), self.B, self.s))
+        else:
+            return gfx950.mul(x.contiguous(), self.B, self.s, out=out)
+        return y if out is None else out.copy_(y)
 
     def silu_mul(self, x: torch.Tensor) -> torch.Tensor:
         """silu(gate) * up of this [gate; up] weight's product, [T, N/2] bf16: one fused launch

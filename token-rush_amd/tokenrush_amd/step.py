@@ -32,9 +32,10 @@ continues from.
 The decode state (tokenrush/state.py:14-43) lives on the device: the position and the committed
 recurrent-state slot (read by the mixers, written by the accept), the conv rings and the fp32
 recurrent state in 8 snapshot slots per GDN layer, and the FP8 KV cache with per-(head, position)
-scales per attention layer, preloaded with `live` random tokens. The step reads its input rows from
-the buffer x0 (what the embedding gather of the verify tokens produces); the embedding table itself
-is kept for checkpoints.
+scales per attention layer, preloaded with `live` random tokens. `verify(spec_toks, ...)` is the
+reference's _verify_step (model.py:293-312) whole: the embedding gather of the verify tokens, the
+body, the lm_head and the accept, keeping spec_logits[:M] and spec_hidden[:M] (the post-final-norm
+rows the draft head reads next, model.py:300-301). `step(x0, ...)` starts from given input rows.
 """
 from dataclasses import dataclass
 
@@ -45,7 +46,7 @@ from .accept import AcceptState, accept_residual, accept_sampled, accept_tree, c
 from .attn import AttnConfig, attn_decode_fused, attn_prep, rope_table
 from .attn import NSPLIT as ATTN_NSPLIT
 from .attn import workspace as attn_workspace
-from .fused import add_rmsnorm
+from .fused import add_rmsnorm, embed_rows
 from .gdn import RING, GDNConfig, gdn_step_fused, tree_commit
 from .gdn import workspace as gdn_workspace
 from .quant import QLinear
@@ -271,6 +272,13 @@ class VerifyModel:
             d = self.attn_index if L.attention else self.gdn_index
             d[li] = len(d)
         self.state = StepState(cfg, len(self.gdn_index), len(self.attn_index), gen, self.device)
+        # the verify step's consumer buffers (model.py:300-301): rows 0..M-1 hold the last step's
+        # logits and post-final-norm hidden; spec_x holds its embedded input rows
+        R = cfg.n_slots
+        self.spec_x = torch.zeros(R, cfg.hidden, dtype=torch.bfloat16, device=self.device)
+        self.spec_hidden = torch.zeros(R, cfg.hidden, dtype=torch.bfloat16, device=self.device)
+        self.spec_logits = torch.zeros(R, cfg.vocab, dtype=torch.bfloat16, device=self.device)
+        self.embed_status = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     def nbytes(self) -> int:
         return self.lm_head.nbytes + sum(L.weight_bytes() for L in self.layers)
@@ -291,8 +299,9 @@ class VerifyModel:
         return gdn_step_fused(u, n, L.in_ba, st.ring[g], L.conv_w, L.A, L.dt_bias, st.rec[:, g], slot_t, L.norm_w,
                               pos_t, cfg.gdn, cfg.eps, parent=parent, node_in=node_in)
 
-    def hidden(self, x0: torch.Tensor, pos_t=None, slot_t=None, parent=None) -> torch.Tensor:
-        """x0 [M, hidden] bf16 -> post-final-norm hidden [M, hidden] bf16 (model.py:252-254)."""
+    def hidden(self, x0: torch.Tensor, pos_t=None, slot_t=None, parent=None, out=None) -> torch.Tensor:
+        """x0 [M, hidden] bf16 -> post-final-norm hidden [M, hidden] bf16 (model.py:252-254),
+        written into out when given."""
         cfg = self.cfg
         pos_t = self.state.pos if pos_t is None else pos_t
         slot_t = self.state.slot if slot_t is None else slot_t
@@ -304,7 +313,7 @@ class VerifyModel:
             h = L.out.partials(self.mixer(li, L, n, pos_t, slot_t, parent))
             x, n = add_rmsnorm(x, h, L.ln2, cfg.eps)
             h = L.down.partials(L.gate_up.silu_mul(n))
-        _, n = add_rmsnorm(x, h, self.final_norm, cfg.eps)
+        _, n = add_rmsnorm(x, h, self.final_norm, cfg.eps, out=out)
         return n
 
     @classmethod
@@ -333,18 +342,22 @@ class VerifyModel:
     def step(self, x0: torch.Tensor, spec_toks: torch.Tensor, st: AcceptState, params: SamplingParams = None,
              u: torch.Tensor = None, q: torch.Tensor = None) -> torch.Tensor:
         """Body at st.pos / st.slot, the lm_head and the accept/commit, which advances st.pos by
-        n + 1 and sets st.slot = n (model.py:293-312). Returns the logits [M, vocab], kept as the
-        reference keeps them (model.py:300; graph-owned under capture). The accept rule:
+        n + 1 and sets st.slot = n (model.py:293-312). Returns the logits [M, vocab]: a view of
+        spec_logits[:M], which keeps them as the reference does (model.py:300), beside
+        spec_hidden[:M] (model.py:301); the next step overwrites both. The accept rule:
           greedy    (params None, q None): in the lm_head GEMM's epilogue, one launch;
           sampled   (params given): pred = sample(logits, params, u) with the device-side
                     SamplingParams and uniforms u [M] (drawn on the device when None, as
                     sample.py:47-48 does), then the leading-match commit (model.py:306-312);
           residual  (q given, fp32 [M - 1, vocab] draft probabilities, u [M]): rejection
                     sampling with the residual resample."""
-        n = self.hidden(x0, st.pos, st.slot)
+        M = x0.shape[0]
+        if M > self.spec_hidden.shape[0]:
+            raise RuntimeError(f"step: {M} rows, room for {self.spec_hidden.shape[0]}")
+        n = self.hidden(x0, st.pos, st.slot, out=self.spec_hidden[:M])
         if params is None and q is None:
-            return lm_head_greedy(self.lm_head, n, spec_toks, st, keep_logits=True)
-        logits = self.lm_head(n)
+            return lm_head_greedy(self.lm_head, n, spec_toks, st, keep_logits=True, out=self.spec_logits[:M])
+        logits = self.lm_head(n, out=self.spec_logits[:M])
         if q is not None:
             if u is None:
                 u = torch.rand(logits.shape[0], device=logits.device)
@@ -353,6 +366,19 @@ class VerifyModel:
             accept_sampled(logits, spec_toks, params, st, u)
         return logits
 
+
+    def verify(self, spec_toks: torch.Tensor, st: AcceptState, params: SamplingParams = None,
+               u: torch.Tensor = None, q: torch.Tensor = None) -> torch.Tensor:
+        """The reference's _verify_step (model.py:293-312) from token ids: spec_toks int64 [M] on
+        the device (the committed token, then M - 1 drafts) are embedded on the device
+        (model.py:215) into spec_x, then step() runs; spec_logits[:M] and spec_hidden[:M] keep the
+        logits and the post-final-norm rows. Capturable as one hipGraph. An id outside the
+        vocabulary embeds as a zero row and sets embed_status to 1."""
+        M = spec_toks.shape[0]
+        if M > self.spec_x.shape[0]:
+            raise RuntimeError(f"verify: {M} rows, room for {self.spec_x.shape[0]}")
+        x0 = embed_rows(self.embed, spec_toks, out=self.spec_x[:M], status=self.embed_status)
+        return self.step(x0, spec_toks, st, params=params, u=u, q=q)
 
     def step_tree(self, x0: torch.Tensor, node_toks: torch.Tensor, parent: torch.Tensor,
                   st: AcceptState) -> torch.Tensor:
