@@ -916,9 +916,13 @@ __device__ __forceinline__ bool arrive_last_wave(int* cnt, int total) {
   __builtin_amdgcn_s_waitcnt(0);
   int last = 0;
   if ((threadIdx.x & 63) == 0) {
+    handoff_release();
     const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = old == total - 1;
-    if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) {
+      __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      handoff_acquire();
+    }
   }
   return __builtin_amdgcn_readfirstlane(last) != 0;
 }

@@ -538,9 +538,13 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   __syncthreads();
   if (tid == 0) {
     int* c = a.cnt + hv * 32;
+    handoff_release();
     const int old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = old == kGdnNVB - 1;
-    if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) {
+      __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      handoff_acquire();
+    }
   }
   __syncthreads();
   if (!last) return;

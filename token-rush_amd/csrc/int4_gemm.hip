@@ -510,9 +510,12 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   __shared__ int last;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
+    handoff_release();
     last = __hip_atomic_fetch_add(a.ws_cnt + rbi * kWsCounterStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
            a.S - 1;
+    if (last) handoff_acquire();
+  }
   __syncthreads();
   if (!last) return;
   // Each thread takes kTailE outputs per pass (two sums each in the pair layout: gate and up)

@@ -19,6 +19,23 @@ enum {
   TR_ERR_SCRATCH = 5,    // the call needs more than the fixed device scratch of a no-allocation entry point
 };
 
+// Ordering of the last-arriver handoffs (a workgroup publishes data, then bumps a counter; the
+// last arriver reads everyone's data). The library's build publishes with agent-scope (sc1)
+// stores, waits for them to complete, passes a workgroup barrier and bumps the counter with a
+// relaxed agent-scope atomic; readers use agent-scope loads. A build with -DTR_FORMAL_FENCES adds
+// the memory model's agent-scope release fence before the counter atomic and acquire fence after
+// it in the last arriver (buffer_wbl2 / buffer_inv on gfx950), for measuring what they cost.
+__device__ __forceinline__ void handoff_release() {
+#ifdef TR_FORMAL_FENCES
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+#endif
+}
+__device__ __forceinline__ void handoff_acquire() {
+#ifdef TR_FORMAL_FENCES
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#endif
+}
+
 // bf16 bits -> fp32 (exact).
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
