@@ -63,3 +63,13 @@ def test_packed_bytes():
     assert lib.tr_packed_bytes(16, 384) == 4352                       # 3 groups padded to one quad
     assert lib.tr_packed_bytes(100, 5120) == 0 and lib.tr_packed_bytes(16, 100) == 0
     assert lib.tr_packed_bytes(1 << 20, 1 << 15) == 0                 # 2 GiB or more: unsupported
+
+
+def test_ext_module_surface():
+    """ext() answers the reference extension module's partial_slots (marlin_bf16.cpp:45-56) with
+    the binding's positional arguments, and still exposes every C-ABI entry point."""
+    from tokenrush_amd import gfx950
+    e = gfx950.ext()
+    for N, K in [(5120, 17408), (5120, 6144), (34816, 5120)]:
+        assert e.partial_slots(N, K) == gfx950.partial_slots(N, K) == e.partial_slots(N, K, -1, -1, -1)
+    assert e.tr_packed_bytes(5120, 5120) == gfx950.ext().tr_packed_bytes(5120, 5120) > 0

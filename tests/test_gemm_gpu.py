@@ -334,3 +334,26 @@ def test_config2_partials_two_row_tiles(dev, N, K, M):
     check_close(part.sum(0), ref, f"partials {N}x{K} M={M}")
     y = gfx950.mul(xd, B, sp, mp).float()
     assert (part.sum(0) - y).abs().max().item() <= np.abs(ref).max() * 2 ** -8
+
+
+def test_ext_mul_binding_semantics(dev):
+    """ext().mul(A, B, C, s, m, workspace, red) as the reference's torch binding calls it
+    (marlin_bf16.cpp:14-44): C bf16 -> the product, C fp32 [slots, m, n] -> the partials; the same
+    bits as gfx950.mul / mul_partial."""
+    from tokenrush_amd import gfx950
+    say("ext().mul binding")
+    p, s, m = o.make_weights(5120, 17408, seed=31, dtype="bf16")
+    x = o.make_x(8, 17408, seed=32)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "bf16"))
+    xd = dev_x(x)
+    ws, _ = gfx950.workspaces(5120, dev, 17408, 8)
+    C = torch.empty(8, 5120, dtype=torch.bfloat16, device=dev)
+    gfx950.ext().mul(xd, B, C, sp, mp, ws, None, -1, -1, -1)
+    S = gfx950.ext().partial_slots(5120, 17408)
+    P = torch.empty(S, 8, 5120, dtype=torch.float32, device=dev)
+    gfx950.ext().mul(xd, B, P, sp, mp, ws, None)
+    torch.cuda.synchronize()
+    assert torch.equal(C, gfx950.mul(xd, B, sp, mp))
+    assert torch.equal(P, gfx950.mul_partial(xd, B, sp, mp))
+    with pytest.raises(RuntimeError):
+        gfx950.ext().mul(xd, B, torch.empty(8, 5120, dtype=torch.float16, device=dev), sp, mp, ws, None)

@@ -18,7 +18,8 @@ design, not Marlin:
   [S, M, N] and mul reduces in the last-arriving workgroup through the workspace.
 
 API (same names and argument meaning as marlin.py): ext, available, pack, unpack,
-workspaces, mul, partial_slots, mul_partial.
+workspaces, mul, partial_slots, mul_partial; ext() also answers the extension module's own
+mul / partial_slots (marlin_bf16.cpp:14-57).
 """
 import ctypes
 
@@ -34,9 +35,52 @@ SCALE_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 WS_COUNTER_BYTES = 4096 * 128   # the workspace's counter region (one counter per 128-byte line)
 
 
+class _Ext:
+    """The loaded library as the reference's compiled extension module (marlin.ext(), the torch
+    binding of marlin_bf16.cpp:14-57): mul(A, B, C, s, m, workspace, red, thread_k, thread_n, sms)
+    and partial_slots(n, k, thread_k, thread_n, sms), with the binding's argument meaning -- C bf16
+    [m, n] is the product, C fp32 [slots, m, n] the split-K partials -- and RuntimeError where the
+    binding's TORCH_CHECKs fail. thread_k / thread_n / sms are accepted and ignored (this kernel
+    plans its own tiling); red is accepted and unused (the workspace holds everything). Every other
+    attribute is the C ABI's entry point of that name (tr_*)."""
+
+    def __init__(self, lib):
+        self._lib = lib
+
+    def __getattr__(self, name):
+        return getattr(self._lib, name)
+
+    def mul(self, A, B, C, s, m, workspace, red=None, thread_k=-1, thread_n=-1, sms=-1):
+        del m, red, thread_k, thread_n, sms
+        M, K = A.shape
+        N = B.shape[0] * 16
+        if C.dtype == torch.float32:
+            if C.dim() != 3 or tuple(C.shape[1:]) != (M, N):
+                raise RuntimeError("partial buffer must be [slots, m, n]")
+            _launch(A, B, s, C, True, C.shape[0])
+        elif C.dtype == torch.bfloat16:
+            if tuple(C.shape) != (M, N) or not C.is_contiguous():
+                raise RuntimeError("C must be bf16 [m, n] (or an fp32 [slots, m, n] partial buffer)")
+            if workspace is not None and workspace.numel() < workspace_bytes(N, K, M):
+                raise RuntimeError("workspace too small")
+            _launch(A, B, s, C, False, 0)
+        else:
+            raise RuntimeError("C must be bf16 (or an fp32 [slots, m, n] partial buffer)")
+
+    def partial_slots(self, n, k, thread_k=-1, thread_n=-1, sms=-1):
+        del thread_k, thread_n, sms
+        return partial_slots(n, k)
+
+
+_ext = None
+
+
 def ext():
-    """The loaded C-ABI library (raises if it is not built)."""
-    return _lib.lib()
+    """The loaded C-ABI library (raises if it is not built), as the reference's extension module."""
+    global _ext
+    if _ext is None:
+        _ext = _Ext(_lib.lib())
+    return _ext
 
 
 def available() -> bool:
