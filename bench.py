@@ -419,7 +419,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer verify-step graph (config 5)")
-    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["config5", "config4", "config1", "lm_head", "accept"],
+    ap.add_argument("--rows", type=int, default=M_VERIFY,
+                    help="profiling aid: the verify rows M of --only <projection | layer_set> (1..32)")
+    ap.add_argument("--only", choices=[n for n, _, _, _ in LAYER_SET] + ["layer_set", "config5", "config4", "config1",
+                                                                       "lm_head", "accept"],
                     help="profiling aid: run just this projection's launches (M=8), or the config-5 step graph, and exit")
     ap.add_argument("--timeline", choices=[n for n, _, _, _ in LAYER_SET],
                     help="profiling aid: the in-kernel timeline of this projection's GEMM at M=8 (needs the "
@@ -468,13 +471,16 @@ def main():
     torch.cuda.synchronize()
 
     if a.only:
-        j = [n for n, _, _, _ in LAYER_SET].index(a.only)
-        x = torch.randn(M_VERIFY, LAYER_SET[j][2], device=dev, generator=gen).to(torch.bfloat16)
+        if not 1 <= a.rows <= 32:
+            raise SystemExit("--rows must be 1..32")
+        js = range(len(LAYER_SET)) if a.only == "layer_set" else [[n for n, _, _, _ in LAYER_SET].index(a.only)]
+        xs = {K: torch.randn(a.rows, K, device=dev, generator=gen).to(torch.bfloat16) for _, _, K, _ in LAYER_SET}
         for _ in range(max(1, a.steps // n_copies)):
             for c in copies:
-                call(gfx950, x, c[j])
+                for j in js:
+                    call(gfx950, xs[LAYER_SET[j][2]], c[j])
         torch.cuda.synchronize()
-        print(json.dumps({"only": a.only, "launches": max(1, a.steps // n_copies) * n_copies}))
+        print(json.dumps({"only": a.only, "rows": a.rows, "launches": max(1, a.steps // n_copies) * n_copies * len(js)}))
         return
 
     slots = {name: (gfx950.partial_slots(N, K, M_VERIFY) if partial else None) for name, N, K, partial in LAYER_SET}
