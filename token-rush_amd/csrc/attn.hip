@@ -119,8 +119,11 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(AttnPrepArgs a) {
   const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
   int dep = t;
   if (a.parent) {
+    // the depth by walking the parents held one per lane (one load for the wave, then shuffles:
+    // a walk of dependent memory loads waited for each)
+    const int pl = lane > 0 && lane < (int)gridDim.y ? attn_tree_parent(a.parent, lane) : 0;
     dep = 0;
-    for (int j = t; j > 0 && dep < kAttnMaxTree; ++dep) j = attn_tree_parent(a.parent, j);
+    for (int j = t; j > 0 && dep < kAttnMaxTree; ++dep) j = __shfl(pl, j);
   }
   // Positions past the cache's end: the rope table (maxlen rows) is read at the last row and no
   // cache row is written (the split kernel reads at most maxlen rows), so nothing outside the
@@ -263,13 +266,16 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(AttnSplitAr
   uint32_t vis = qi >= 31 ? ~0u : (2u << qi) - 1u;
   const int64_t qlimit = pos + qi;  // a chain's last visible row
   if (TREE) {
+    // the parents one per lane (one load for the wave), then the walk by shuffles
+    const int pl = lane > 0 && lane < a.M ? attn_tree_parent(a.parent, lane) : 0;
     vis = 0;
     int jn = qi;
     for (int d = 0; d < kAttnMaxTree; ++d) {
       vis |= 1u << jn;
-      if (jn == 0) break;
-      jn = attn_tree_parent(a.parent, jn);
+      jn = __shfl(pl, jn);  // the root's entry is 0
+      if (__all(jn == 0)) break;
     }
+    vis |= 1u;  // the root: every node sees it
   }
 
   f32x4 acc[16];

@@ -153,6 +153,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
   __shared__ float part[4][8];
   __shared__ float ssq[4][TG];
   __shared__ int src_s[MAXM][3];  // window inputs of token t, 1..3 back: a token, or -(ring slot + 1)
+  __shared__ int par_l[MAXM];     // a tree's parents, loaded once (the walks below run in LDS)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = a.M;
   const int QK = a.H * kGdnK;
@@ -172,16 +173,20 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
     const int ch = cb * kGdnThreads + tid;
     const bool on = ch < C;
     const int pr = (int)(*a.pos % a.R);  // ring column of token 0
+    if (TREE) {
+      if (tid < M) par_l[tid] = tid == 0 ? 0 : tree_parent(a.parent, tid);
+      __syncthreads();
+    }
     if (TREE && tid < M) {
       int j = tid, dep = 0;
       for (int s = 0; s < MAXM && j > 0; ++s) {
-        j = tree_parent(a.parent, j);
+        j = par_l[j];
         ++dep;
       }
       j = tid;
       for (int k = 0; k < 3; ++k) {  // k + 1 back
         if (dep > k) {
-          j = tree_parent(a.parent, j);
+          j = par_l[j];
           src_s[tid][k] = j;
         } else {
           src_s[tid][k] = -(3 - (k + 1 - dep)) - 1;  // position pos - (k + 1 - dep): ring slot 3 - (k + 1 - dep)
