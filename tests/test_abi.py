@@ -73,3 +73,16 @@ def test_ext_module_surface():
     for N, K in [(5120, 17408), (5120, 6144), (34816, 5120)]:
         assert e.partial_slots(N, K) == gfx950.partial_slots(N, K) == e.partial_slots(N, K, -1, -1, -1)
     assert e.tr_packed_bytes(5120, 5120) == gfx950.ext().tr_packed_bytes(5120, 5120) > 0
+
+
+def test_tree_split_count_fits_one_round():
+    """A draft tree's flash-decoding grid (kv heads x splits x 64-row groups) fits the split
+    kernel's resident slots in one round; chains and small trees keep NSPLIT."""
+    from tokenrush_amd import attn
+    cfg = attn.AttnConfig()
+    assert attn.tree_splits(32, cfg) == 42                     # 4 x 42 x 3 = 504 <= 512
+    assert attn.tree_splits(10, cfg) == attn.NSPLIT            # 60 rows: one group
+    for M in range(1, 33):
+        s = attn.tree_splits(M, cfg)
+        groups = -(-6 * M // 64)
+        assert 1 <= s <= attn.NSPLIT and cfg.n_kv_heads * s * groups <= attn.SPLIT_SLOTS

@@ -16,6 +16,17 @@ from . import _lib
 
 NSPLIT = 64        # key-range splits of the flash-decoding kernel: 256 workgroups at 4 kv heads
                    # (the reference uses 32 on a 170-SM part; measured fastest here)
+CHAIN_NSPLIT = NSPLIT
+SPLIT_SLOTS = 512  # split-kernel workgroups resident at once: 256 CUs, two each (240 registers a lane)
+
+
+def tree_splits(M: int, cfg) -> int:
+    """Key-range splits for a draft tree of M nodes: its G M query rows per kv head run in groups of
+    64 (a second grid dimension), so the grid is HKV x splits x groups; the largest count up to
+    NSPLIT whose grid fits one round of SPLIT_SLOTS (42 for 32 nodes at 24 / 4 heads: 21% faster
+    per call than 64, which needs a second round)."""
+    groups = -(-(cfg.n_heads // cfg.n_kv_heads) * M // 64)
+    return max(1, min(NSPLIT, SPLIT_SLOTS // (cfg.n_kv_heads * groups)))
 
 
 @dataclass(frozen=True)
@@ -102,12 +113,13 @@ def workspace(M: int, HQ: int, nsplit: int, device):
     return _lib.grown_workspace(_ws, key, need, device, zero=False)
 
 
-def attn_decode_fused(q, qkv, k_cache, v_cache, pos_t, cfg, k_scale=None, v_scale=None, NSPLIT=NSPLIT,
+def attn_decode_fused(q, qkv, k_cache, v_cache, pos_t, cfg, k_scale=None, v_scale=None, NSPLIT=None,
                       parent=None):
     """q [M, HQ D] (from attn_prep) for the M new tokens at pos.., qkv [M, ..] (for the gates)
     -> gated attention output [M, HQ D] bf16; query t sees cache rows <= pos + t
     (fused.py:448-470). With parent (a draft tree of M <= 32 nodes, as attn_prep), node t sees
-    the rows before pos and the rows pos + i of its ancestors and itself."""
+    the rows before pos and the rows pos + i of its ancestors and itself. NSPLIT (key-range
+    splits) defaults to NSPLIT for a chain and to tree_splits(M, cfg) for a tree."""
     _lib.require_gpu(q, qkv, k_cache, v_cache, pos_t)
     _check_cache(k_cache, v_cache, k_scale, v_scale, cfg)
     if q.dtype != torch.bfloat16 or not q.is_contiguous() or qkv.dtype != torch.bfloat16 or qkv.stride(1) != 1:
@@ -115,6 +127,8 @@ def attn_decode_fused(q, qkv, k_cache, v_cache, pos_t, cfg, k_scale=None, v_scal
     M = q.shape[0]
     HQ, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
     out = torch.empty(M, HQ * D, device=q.device, dtype=torch.bfloat16)
+    if NSPLIT is None:
+        NSPLIT = CHAIN_NSPLIT if parent is None else tree_splits(M, cfg)
     ws = workspace(M, HQ, NSPLIT, q.device)
     ld = qkv.stride(0) if M > 1 else qkv.shape[1]
     par = _parent(parent, M, q.device)
