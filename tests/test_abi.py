@@ -75,9 +75,9 @@ def test_ext_module_surface():
     assert e.tr_packed_bytes(5120, 5120) == gfx950.ext().tr_packed_bytes(5120, 5120) > 0
 
 
-def test_tree_split_count_fits_one_round():
+def test_tree_split_count_fits_one_pass():
     """A draft tree's flash-decoding grid (kv heads x splits x 64-row groups) fits the split
-    kernel's resident slots in one round; chains and small trees keep NSPLIT."""
+    kernel's resident slots in one pass; chains and small trees keep NSPLIT."""
     from tokenrush_amd import attn
     cfg = attn.AttnConfig()
     assert attn.tree_splits(32, cfg) == 42                     # 4 x 42 x 3 = 504 <= 512

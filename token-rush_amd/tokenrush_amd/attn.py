@@ -23,8 +23,8 @@ SPLIT_SLOTS = 512  # split-kernel workgroups resident at once: 256 CUs, two each
 def tree_splits(M: int, cfg) -> int:
     """Key-range splits for a draft tree of M nodes: its G M query rows per kv head run in groups of
     64 (a second grid dimension), so the grid is HKV x splits x groups; the largest count up to
-    NSPLIT whose grid fits one round of SPLIT_SLOTS (42 for 32 nodes at 24 / 4 heads: 21% faster
-    per call than 64, which needs a second round)."""
+    NSPLIT whose grid fits one pass of SPLIT_SLOTS (42 for 32 nodes at 24 / 4 heads: 21% faster
+    per call than 64, which needs a second pass)."""
     groups = -(-(cfg.n_heads // cfg.n_kv_heads) * M // 64)
     return max(1, min(NSPLIT, SPLIT_SLOTS // (cfg.n_kv_heads * groups)))
 
