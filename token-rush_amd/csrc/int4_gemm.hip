@@ -725,6 +725,32 @@ int group_block(int M) { return M > 16 ? 2 : 4; }
 
 // Tiling of an N x K weight for M rows. Depends on M only through the row-tile count
 // (M <= 16 or not), so rows are bit-identical for every M within each range.
+bool make_plan(int N, int K, int M, int S_req, int R_req, Plan* p);
+
+// The partial-mode plan (the caller sums the slots, so more K slots cost only their writes, not
+// a last-arriver slot sum): the slot count from the default's up to 6 with the least work on the
+// busiest CU, ceil(workgroups / CUs) x strips x waves, the smaller count on ties. Measured at
+// M = 8 (graph of launches, us): the 5120 x 6144 projection 7.62 at the default 1 slot, 6.72 at
+// the chosen 3; 5120 x 17408 12.38 at 3, 12.0 at the chosen 4.
+bool make_partial_plan(int N, int K, int M, Plan* p) {
+  Plan best;
+  if (!make_plan(N, K, M, 0, 0, &best)) return false;
+  long best_cost = -1;
+  const int s_max = 6;
+  for (int S = best.S; S <= s_max; ++S) {
+    Plan q;
+    if (!make_plan(N, K, M, S, 0, &q)) continue;
+    const long grid = (long)q.grid_n * q.S;
+    const long cost = (grid + kCUs - 1) / kCUs * q.R * q.W;
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = q;
+    }
+  }
+  *p = best;
+  return true;
+}
+
 bool make_plan(int N, int K, int M, int S_req, int R_req, Plan* p) {
   const int nstrips = N / 16;
   p->GW = group_block(M);
@@ -803,9 +829,9 @@ int tr_gemm_plan(int N, int K, int M, int* S, int* W, int* R) {
 size_t tr_packed_bytes(int N, int K) { return shape_ok(N, K) ? packed_bytes(N, K) : 0; }
 
 int tr_partial_slots(int N, int K, int M) {
-  int S, W, R;
-  if (tr_gemm_plan(N, K, M, &S, &W, &R)) return -1;
-  return S;
+  Plan p;
+  if (!shape_ok(N, K) || M < 1 || M > 32 || !make_partial_plan(N, K, M, &p)) return -1;
+  return p.S;
 }
 
 // Workspace of an out-mode call with S > 1: kWsCounters int32 counters at offset 0 -- a fixed
