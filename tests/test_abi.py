@@ -86,3 +86,18 @@ def test_tree_split_count_fits_one_pass():
         s = attn.tree_splits(M, cfg)
         groups = -(-6 * M // 64)
         assert 1 <= s <= attn.NSPLIT and cfg.n_kv_heads * s * groups <= attn.SPLIT_SLOTS
+
+
+def test_partial_plan_is_host_only_and_independent_of_m():
+    """The partial-mode plan (the caller sums the slots): between the out-mode plan's slot
+    count and 6, depending on M only through the row-tile range, and the slot counts measured
+    fastest for the o and down projections (3 and 4 below 17 rows)."""
+    from tokenrush_amd import gfx950
+    for N, K in [(5120, 5120), (7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (16, 128), (512, 17408)]:
+        for M in (1, 8, 16, 17, 32):
+            S = gfx950.partial_slots(N, K, M)
+            S0 = gfx950.plan(N, K, M)[0]
+            assert S0 <= S <= max(S0, 6), (N, K, M, S, S0)
+            assert gfx950.partial_slots(N, K, 1 if M <= 16 else 32) == S
+    assert gfx950.partial_slots(5120, 6144, 8) == 3 and gfx950.partial_slots(5120, 17408, 8) == 4
+    assert gfx950.partial_slots(5120, 17408, 32) == gfx950.plan(5120, 17408, 32)[0] == 6
