@@ -431,98 +431,238 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float kk = ck[0][k0 + j];
-      p.x += S[j].x * kk;
-      p.y += S[j].y * kk;
+      p.x = fmaf(S[j].x, kk, p.x);
+      p.y = fmaf(S[j].y, kk, p.y);
     }
     kv = wsum(p, 0);
   }
   float* const obase = a.o_ws + (size_t)hv * kGdnV + v0;
   const size_t head_off = (size_t)hv * kGdnK * kGdnV + v0;
-  for (int i = 0; i < M; ++i) {
-    // wave-uniform values from LDS, kept in scalar registers
-    const int t = TREE ? __builtin_amdgcn_readfirstlane(ord_s[i]) : i;
-    const int tn = i + 1 < M ? (TREE ? __builtin_amdgcn_readfirstlane(ord_s[i + 1]) : i + 1) : t;  // the next node
-    const int pn = TREE && i + 1 < M ? __builtin_amdgcn_readfirstlane(par_s[tn]) : t;  // ... continues from
-    const float beta = beta_s[t], eg = decay_s[t];
-    const float* vt = &cv[t][c0];
-    float2 dv;
-    dv.x = beta * (vt[0] - eg * kv.x);
-    dv.y = beta * (vt[1] - eg * kv.y);
-    float2 o = make_float2(0.f, 0.f), nx = o;
-    float* dst = a.rec + (size_t)t * a.slot_stride + head_off;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float kk = ck[t][k0 + j], qq = cq[t][k0 + j];
-      S[j].x = S[j].x * eg + kk * dv.x;
-      S[j].y = S[j].y * eg + kk * dv.y;
-      // non-temporal: of the M snapshots only the accepted one is read again (by the next step)
-      __builtin_nontemporal_store(S[j].x, dst + (size_t)(k0 + j) * kGdnV);
-      __builtin_nontemporal_store(S[j].y, dst + (size_t)(k0 + j) * kGdnV + 1);
-      o.x += S[j].x * qq;
-      o.y += S[j].y * qq;
+  if constexpr (TREE) {
+    // Each node's wave-uniform values (its index in the visiting order, the next node, the node
+    // that one continues from, depths, branch flag, beta and the decay) sit in lane i of a
+    // register for visit i (M <= 32 lanes), read with v_readlane: the loop makes no LDS round
+    // trip for them, where a readfirstlane of an LDS value stalled the wave (one per SIMD) for
+    // each. The node's rows of v, k and q and the next node's k row are read from LDS one visit
+    // ahead, under the previous visit's work.
+    int T_l = 0, TN_l = 0, PN_l = 0, DT_l = 0, BT_l = 0, DPN_l = 0;
+    float BE_l = 0.f, EG_l = 0.f;
+    if (lane < M) {
+      T_l = TREE ? ord_s[lane] : lane;
+      TN_l = lane + 1 < M ? (TREE ? ord_s[lane + 1] : lane + 1) : T_l;
+      PN_l = TREE && lane + 1 < M ? par_s[TN_l] : T_l;
+      if (TREE) {
+        DT_l = dep_s[T_l];
+        BT_l = br_s[T_l];
+        DPN_l = dep_s[PN_l];
+      }
+      BE_l = beta_s[T_l];
+      EG_l = decay_s[T_l];
     }
-    if (TREE && __builtin_amdgcn_readfirstlane(br_s[t])) {  // a branch node, visited again for its later children
-      const int d = __builtin_amdgcn_readfirstlane(dep_s[t]);
-#pragma unroll
-      for (int e = 0; e < kStk; ++e)
-        if (e == d)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) stk[e][j] = S[j];
-    }
-    // the next node's k product from the state it starts from: this node's, or an earlier one's.
-    // The snapshot-load path waits for its loads itself: a load still pending where the paths
-    // meet would make every path wait for the memory counter, i.e. for this node's stores.
-    auto next_sum = [&]() {
+    auto lane_i = [](int v, int i) { return __builtin_amdgcn_readlane(v, i); };
+    auto lane_f = [](float v, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i)); };
+    // visit 0's rows
+    float2 vt;
+    float kk[4], qq[4], kn[4];
+    {
+      const int t = lane_i(T_l, 0), tn = lane_i(TN_l, 0);
+      vt = *(const float2*)&cv[t][c0];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float kn = ck[tn][k0 + j];
-        nx.x += S[j].x * kn;
-        nx.y += S[j].y * kn;
+        kk[j] = ck[t][k0 + j];
+        qq[j] = cq[t][k0 + j];
+        kn[j] = ck[tn][k0 + j];
       }
-    };
-    if (!TREE || pn == t) {
-      next_sum();
-    } else {
-      const int d = __builtin_amdgcn_readfirstlane(dep_s[pn]);
-      if (d < kStk) {
+    }
+    for (int i = 0; i < M; ++i) {
+      const int t = lane_i(T_l, i), tn = lane_i(TN_l, i);
+      const int pn = TREE ? lane_i(PN_l, i) : t;  // the node the next one continues from
+      const float beta = lane_f(BE_l, i), eg = lane_f(EG_l, i);
+      float2 dv;
+      dv.x = beta * fmaf(-eg, kv.x, vt.x);
+      dv.y = beta * fmaf(-eg, kv.y, vt.y);
+      // the next visit's rows (its node is tn; its next node's k row), read under this visit's work
+      float2 vt1;
+      float qq1[4], kn1[4];
+      {
+        const int tn1 = lane_i(TN_l, i + 1 < M ? i + 1 : i);
+        vt1 = *(const float2*)&cv[tn][c0];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          qq1[j] = cq[tn][k0 + j];
+          kn1[j] = ck[tn1][k0 + j];
+        }
+      }
+      float2 o = make_float2(0.f, 0.f), nx = o;
+      float* dst = a.rec + (size_t)t * a.slot_stride + head_off;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        S[j].x = fmaf(kk[j], dv.x, __fmul_rn(S[j].x, eg));
+        S[j].y = fmaf(kk[j], dv.y, __fmul_rn(S[j].y, eg));
+        // non-temporal: of the M snapshots only the accepted one is read again (by the next step)
+        __builtin_nontemporal_store(S[j].x, dst + (size_t)(k0 + j) * kGdnV);
+        __builtin_nontemporal_store(S[j].y, dst + (size_t)(k0 + j) * kGdnV + 1);
+        o.x = fmaf(S[j].x, qq[j], o.x);
+        o.y = fmaf(S[j].y, qq[j], o.y);
+      }
+      if (TREE && lane_i(BT_l, i)) {  // a branch node, visited again for its later children
+        const int d = lane_i(DT_l, i);
 #pragma unroll
         for (int e = 0; e < kStk; ++e)
           if (e == d)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) S[j] = stk[e][j];
+            for (int j = 0; j < 4; ++j) stk[e][j] = S[j];
+      }
+      // the next node's k product from the state it starts from: this node's, or an earlier one's.
+      // The snapshot-load path waits for its loads itself: a load still pending where the paths
+      // meet would make every path wait for the memory counter, i.e. for this node's stores.
+      auto next_sum = [&]() {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          nx.x = fmaf(S[j].x, kn[j], nx.x);
+          nx.y = fmaf(S[j].y, kn[j], nx.y);
+        }
+      };
+      if (!TREE || pn == t) {
         next_sum();
       } else {
-        const float* src = a.rec + (size_t)pn * a.slot_stride + head_off;
+        const int d = lane_i(DPN_l, i);
+        if (d < kStk) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S[j] = *(const float2*)(src + (size_t)(k0 + j) * kGdnV);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) here, so the paths meet with no load pending
-        next_sum();
+          for (int e = 0; e < kStk; ++e)
+            if (e == d)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) S[j] = stk[e][j];
+          next_sum();
+        } else {
+          const float* src = a.rec + (size_t)pn * a.slot_stride + head_off;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) S[j] = *(const float2*)(src + (size_t)(k0 + j) * kGdnV);
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) here, so the paths meet with no load pending
+          next_sum();
+        }
+      }
+      // both sums in one exchange: buffer (i + 1) % 2 alternates so the next node's writes never
+      // race this node's reads (the barrier between them separates them)
+      o = make_float2(ksum(o.x), ksum(o.y));
+      nx = make_float2(ksum(nx.x), ksum(nx.y));
+      const int buf = (i + 1) & 1;
+      if (kg == 0) {
+        red[buf][wave][vq] = o;
+        red_n[buf][wave][vq] = nx;
+      }
+      __syncthreads();
+      float2 ro = red[buf][0][vq], rn = red_n[buf][0][vq];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float2 u = red[buf][w][vq], q2 = red_n[buf][w][vq];
+        ro.x += u.x;
+        ro.y += u.y;
+        rn.x += q2.x;
+        rn.y += q2.y;
+      }
+      kv = rn;
+      if (wave == 0 && kg == 0) {
+        float* op = obase + (size_t)t * VAL;
+        ws_st(op + 0, bf16r(ro.x));
+        ws_st(op + 1, bf16r(ro.y));
+      }
+      // the next visit's rows: its k row is this visit's next-node row
+      vt = vt1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kk[j] = kn[j];
+        qq[j] = qq1[j];
+        kn[j] = kn1[j];
       }
     }
-    // both sums in one exchange: buffer (i + 1) % 2 alternates so the next node's writes never
-    // race this node's reads (the barrier inside wsum separates them)
-    o = make_float2(ksum(o.x), ksum(o.y));
-    nx = make_float2(ksum(nx.x), ksum(nx.y));
-    const int buf = (i + 1) & 1;
-    if (kg == 0) {
-      red[buf][wave][vq] = o;
-      red_n[buf][wave][vq] = nx;
-    }
-    __syncthreads();
-    float2 ro = red[buf][0][vq], rn = red_n[buf][0][vq];
+  } else {  // a chain: node i is token i, and its values are read where they are used
+    for (int i = 0; i < M; ++i) {
+      // wave-uniform values from LDS, kept in scalar registers
+      const int t = TREE ? __builtin_amdgcn_readfirstlane(ord_s[i]) : i;
+      const int tn = i + 1 < M ? (TREE ? __builtin_amdgcn_readfirstlane(ord_s[i + 1]) : i + 1) : t;  // the next node
+      const int pn = TREE && i + 1 < M ? __builtin_amdgcn_readfirstlane(par_s[tn]) : t;  // ... continues from
+      const float beta = beta_s[t], eg = decay_s[t];
+      const float* vt = &cv[t][c0];
+      float2 dv;
+      dv.x = beta * fmaf(-eg, kv.x, vt[0]);
+      dv.y = beta * fmaf(-eg, kv.y, vt[1]);
+      float2 o = make_float2(0.f, 0.f), nx = o;
+      float* dst = a.rec + (size_t)t * a.slot_stride + head_off;
 #pragma unroll
-    for (int w = 1; w < 4; ++w) {
-      const float2 u = red[buf][w][vq], q2 = red_n[buf][w][vq];
-      ro.x += u.x;
-      ro.y += u.y;
-      rn.x += q2.x;
-      rn.y += q2.y;
-    }
-    kv = rn;
-    if (wave == 0 && kg == 0) {
-      float* op = obase + (size_t)t * VAL;
-      ws_st(op + 0, bf16r(ro.x));
-      ws_st(op + 1, bf16r(ro.y));
+      for (int j = 0; j < 4; ++j) {
+        const float kk = ck[t][k0 + j], qq = cq[t][k0 + j];
+        S[j].x = fmaf(kk, dv.x, __fmul_rn(S[j].x, eg));
+        S[j].y = fmaf(kk, dv.y, __fmul_rn(S[j].y, eg));
+        // non-temporal: of the M snapshots only the accepted one is read again (by the next step)
+        __builtin_nontemporal_store(S[j].x, dst + (size_t)(k0 + j) * kGdnV);
+        __builtin_nontemporal_store(S[j].y, dst + (size_t)(k0 + j) * kGdnV + 1);
+        o.x = fmaf(S[j].x, qq, o.x);
+        o.y = fmaf(S[j].y, qq, o.y);
+      }
+      if (TREE && __builtin_amdgcn_readfirstlane(br_s[t])) {  // a branch node, visited again for its later children
+        const int d = __builtin_amdgcn_readfirstlane(dep_s[t]);
+#pragma unroll
+        for (int e = 0; e < kStk; ++e)
+          if (e == d)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) stk[e][j] = S[j];
+      }
+      // the next node's k product from the state it starts from: this node's, or an earlier one's.
+      // The snapshot-load path waits for its loads itself: a load still pending where the paths
+      // meet would make every path wait for the memory counter, i.e. for this node's stores.
+      auto next_sum = [&]() {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float kn = ck[tn][k0 + j];
+          nx.x = fmaf(S[j].x, kn, nx.x);
+          nx.y = fmaf(S[j].y, kn, nx.y);
+        }
+      };
+      if (!TREE || pn == t) {
+        next_sum();
+      } else {
+        const int d = __builtin_amdgcn_readfirstlane(dep_s[pn]);
+        if (d < kStk) {
+#pragma unroll
+          for (int e = 0; e < kStk; ++e)
+            if (e == d)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) S[j] = stk[e][j];
+          next_sum();
+        } else {
+          const float* src = a.rec + (size_t)pn * a.slot_stride + head_off;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) S[j] = *(const float2*)(src + (size_t)(k0 + j) * kGdnV);
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) here, so the paths meet with no load pending
+          next_sum();
+        }
+      }
+      // both sums in one exchange: buffer (i + 1) % 2 alternates so the next node's writes never
+      // race this node's reads (the barrier inside wsum separates them)
+      o = make_float2(ksum(o.x), ksum(o.y));
+      nx = make_float2(ksum(nx.x), ksum(nx.y));
+      const int buf = (i + 1) & 1;
+      if (kg == 0) {
+        red[buf][wave][vq] = o;
+        red_n[buf][wave][vq] = nx;
+      }
+      __syncthreads();
+      float2 ro = red[buf][0][vq], rn = red_n[buf][0][vq];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float2 u = red[buf][w][vq], q2 = red_n[buf][w][vq];
+        ro.x += u.x;
+        ro.y += u.y;
+        rn.x += q2.x;
+        rn.y += q2.y;
+      }
+      kv = rn;
+      if (wave == 0 && kg == 0) {
+        float* op = obase + (size_t)t * VAL;
+        ws_st(op + 0, bf16r(ro.x));
+        ws_st(op + 1, bf16r(ro.y));
+      }
     }
   }
 
