@@ -240,7 +240,9 @@ __device__ __forceinline__ int udiv_small(uint32_t q, int d, uint32_t magic) {
 // column n = 16 strip + lane % 16.
 template <int MT, int GW, bool F16S, bool XDMA>
 __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
-  extern __shared__ float red[];  // [2][RB][W][MT][64][4]
+  // 16-byte aligned: the dynamic area follows the kernel's 776 bytes of static LDS, and the
+  // ring's and staging area's 16-byte accesses stall when misaligned (SQ_LDS_UNALIGNED_STALL)
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [2][RB][W][MT][64][4]
   TLM(0);
   __shared__ uint64_t rowbest[32];  // fused argmax: best key per output row
   if (threadIdx.x < 32) rowbest[threadIdx.x] = 0;
