@@ -332,7 +332,8 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
   __shared__ float cq[MAXM][kGdnK], ck[MAXM][kGdnK], cv[MAXM][kGdnBV];
   __shared__ float beta_s[MAXM], decay_s[MAXM];
   __shared__ int par_s[MAXM], ord_s[MAXM], dep_s[MAXM], br_s[MAXM];
-  __shared__ float2 red[2][4][8], red_n[2][4][8];
+  __shared__ float2 red[2][4][8];
+  __shared__ __attribute__((aligned(16))) float4 red4[2][4][8];  // [buffer][wave][column pair]: o.x, o.y, kv.x, kv.y
   __shared__ int last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hv = blockIdx.x / kGdnNVB, vb = blockIdx.x % kGdnNVB;
@@ -544,23 +545,21 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
       }
       // both sums in one exchange: buffer (i + 1) % 2 alternates so the next node's writes never
       // race this node's reads (the barrier between them separates them)
-      o = make_float2(ksum(o.x), ksum(o.y));
-      nx = make_float2(ksum(nx.x), ksum(nx.y));
+      // the four sums in one pass: lane row j (lanes 16 j ..) holds o.x, o.y, nx.x, nx.y for j = 0..3
+      const float tot = sum_x8_16_32_4(o.x, o.y, nx.x, nx.y);
       const int buf = (i + 1) & 1;
-      if (kg == 0) {
-        red[buf][wave][vq] = o;
-        red_n[buf][wave][vq] = nx;
-      }
+      if ((kg & 1) == 0) ((float*)&red4[buf][wave][vq])[kg >> 1] = tot;
       __syncthreads();
-      float2 ro = red[buf][0][vq], rn = red_n[buf][0][vq];
+      float4 r4 = red4[buf][0][vq];
 #pragma unroll
       for (int w = 1; w < 4; ++w) {
-        const float2 u = red[buf][w][vq], q2 = red_n[buf][w][vq];
-        ro.x += u.x;
-        ro.y += u.y;
-        rn.x += q2.x;
-        rn.y += q2.y;
+        const float4 u = red4[buf][w][vq];
+        r4.x += u.x;
+        r4.y += u.y;
+        r4.z += u.z;
+        r4.w += u.w;
       }
+      const float2 ro = make_float2(r4.x, r4.y), rn = make_float2(r4.z, r4.w);
       kv = rn;
       if (wave == 0 && kg == 0) {
         float* op = obase + (size_t)t * VAL;
@@ -640,23 +639,21 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_step_kernel(GdnArgs a) {
       }
       // both sums in one exchange: buffer (i + 1) % 2 alternates so the next node's writes never
       // race this node's reads (the barrier inside wsum separates them)
-      o = make_float2(ksum(o.x), ksum(o.y));
-      nx = make_float2(ksum(nx.x), ksum(nx.y));
+      // the four sums in one pass: lane row j (lanes 16 j ..) holds o.x, o.y, nx.x, nx.y for j = 0..3
+      const float tot = sum_x8_16_32_4(o.x, o.y, nx.x, nx.y);
       const int buf = (i + 1) & 1;
-      if (kg == 0) {
-        red[buf][wave][vq] = o;
-        red_n[buf][wave][vq] = nx;
-      }
+      if ((kg & 1) == 0) ((float*)&red4[buf][wave][vq])[kg >> 1] = tot;
       __syncthreads();
-      float2 ro = red[buf][0][vq], rn = red_n[buf][0][vq];
+      float4 r4 = red4[buf][0][vq];
 #pragma unroll
       for (int w = 1; w < 4; ++w) {
-        const float2 u = red[buf][w][vq], q2 = red_n[buf][w][vq];
-        ro.x += u.x;
-        ro.y += u.y;
-        rn.x += q2.x;
-        rn.y += q2.y;
+        const float4 u = red4[buf][w][vq];
+        r4.x += u.x;
+        r4.y += u.y;
+        r4.z += u.z;
+        r4.w += u.w;
       }
+      const float2 ro = make_float2(r4.x, r4.y), rn = make_float2(r4.z, r4.w);
       kv = rn;
       if (wave == 0 && kg == 0) {
         float* op = obase + (size_t)t * VAL;

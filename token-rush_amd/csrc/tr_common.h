@@ -131,6 +131,24 @@ __device__ __forceinline__ float sum_x32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+// Four sums over the lanes l, l ^ 8, l ^ 16, l ^ 32 at once. A permlane swap exchanges the odd
+// rows (halves) of one register with the even rows (halves) of another, so one swap and one add
+// reduce two values at a time: a's pair sums land in the even rows and b's in the odd ones, then
+// the two results' halves are combined the same way. Each lane returns one total: a in row 0
+// (lanes 0-15), b in row 1, c in row 2, d in row 3. Every total is added in the same order as
+// sum_x32(sum_x16(sum_x8(v))) adds it, so it has the same bits.
+__device__ __forceinline__ float sum_x8_16_32_4(float a, float b, float c, float d) {
+  a = sum_x8(a);
+  b = sum_x8(b);
+  c = sum_x8(c);
+  d = sum_x8(d);
+  const auto r1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const auto r2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+  const float ab = __uint_as_float(r1[0]) + __uint_as_float(r1[1]);
+  const float cd = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
+  const auto r3 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ab), __float_as_uint(cd), false, false);
+  return __uint_as_float(r3[0]) + __uint_as_float(r3[1]);
+}
 // the 32 lanes of the same parity (l % 2): quad xor 2, row_ror 4, row_ror 8, row pairs, halves
 __device__ __forceinline__ float sum_parity(float v) {
   v = v + dpp_mov<0x4E>(v);
