@@ -52,6 +52,9 @@ constexpr int kGdnMaxM = 8;  // tokens per chain step (the reference's MP, fused
 constexpr int kGdnMaxTree = 32;  // nodes per draft-tree step
 // tokens per conv workgroup of the prep: all of a chain step's, 4 of a larger tree's
 template <int MAXM> constexpr int gdn_tg() { return MAXM <= 8 ? 8 : 4; }
+// A workgroup barrier that orders LDS accesses only: __syncthreads' workgroup fence also waits
+// for the wave's global loads still in flight, which the prep's early loads must not.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 constexpr int kGdnThreads = 256;
 static_assert(kGdnBV == 16, "the step kernel's lane layout: 8 column pairs");
 
@@ -173,9 +176,27 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
     const int ch = cb * kGdnThreads + tid;
     const bool on = ch < C;
     const int pr = (int)(*a.pos % a.R);  // ring column of token 0
+    // A tree's windows come from ancestors that the parent walks below name: every node's input
+    // of this channel is loaded first (independent of the tree's shape, so the loads' latency
+    // runs under the walks) and staged in LDS, where the windows read them.
+    __shared__ uint16_t nv_s[TREE ? MAXM : 1][kGdnThreads];
+    uint16_t nv[TREE ? MAXM : 1];
+    // The parents first (the walks wait for them, and vector loads complete in issue order), then
+    // the conv weights and the ring's committed inputs. Every thread loads, at a clamped channel
+    // (a load under a branch would be waited for where the paths meet).
+    const int chc = on ? ch : C - 1;
+    const int par_raw = TREE ? a.parent[min(tid, M - 1)] : 0;
+    asm volatile("" ::: "memory");  // issued before the loads below
+    const uint2 wu = *(const uint2*)(a.conv_w + (size_t)chc * 4);
+    uint16_t* rrow = a.ring + (size_t)chc * a.R;
+    uint16_t rr[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) rr[j] = rrow[(pr + j - 3 + a.R) % a.R];  // pos - 3 + j
     if (TREE) {
-      if (tid < M) par_l[tid] = tid == 0 ? 0 : tree_parent(a.parent, tid);
-      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < MAXM; ++u) nv[u] = a.qkvz[(size_t)min(u, M - 1) * a.ld + chc];
+      if (tid < M) par_l[tid] = tid > 0 && par_raw >= 0 && par_raw < tid ? par_raw : 0;  // tree_parent's rule
+      lds_barrier();
     }
     if (TREE && tid < M) {
       int j = tid, dep = 0;
@@ -193,30 +214,32 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnArgs a) {
         }
       }
     }
-    if (TREE) __syncthreads();
+    if (TREE) {
+#pragma unroll
+      for (int u = 0; u < MAXM; ++u) nv_s[u][tid] = nv[u];
+      lds_barrier();
+    }
     float y[TG];
 #pragma unroll
     for (int u = 0; u < TG; ++u) y[u] = 0.f;
     if (on) {
-      const uint2 wu = *(const uint2*)(a.conv_w + (size_t)ch * 4);
       const float w0 = bf16_bits_to_f32(wu.x & 0xFFFFu), w1 = bf16_bits_to_f32(wu.x >> 16);
       const float w2 = bf16_bits_to_f32(wu.y & 0xFFFFu), w3 = bf16_bits_to_f32(wu.y >> 16);
-      uint16_t* rrow = a.ring + (size_t)ch * a.R;
-      // every load first: the ring's committed inputs, the tokens' own and (trees) the windows'
+      // the tokens' own inputs and (trees) the windows', every load first
       float win[TG + 3];  // chain: positions pos - 3 .. pos + TG - 1
       uint16_t xin[TG], wt[TG][3];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) win[j] = bf16_bits_to_f32(rrow[(pr + j - 3 + a.R) % a.R]);  // pos - 3 + j
+      for (int j = 0; j < 3; ++j) win[j] = bf16_bits_to_f32(rr[j]);
 #pragma unroll
       for (int u = 0; u < TG; ++u) {
         const int t = min(t0 + u, M - 1);
-        xin[u] = a.qkvz[(size_t)t * a.ld + ch];
+        xin[u] = TREE ? nv_s[t][tid] : a.qkvz[(size_t)t * a.ld + ch];
         win[u + 3] = bf16_bits_to_f32(t0 + u < M ? xin[u] : (uint16_t)0);
         if (TREE)
 #pragma unroll
           for (int k = 0; k < 3; ++k) {
             const int sn = src_s[t][k];
-            wt[u][k] = sn >= 0 ? a.qkvz[(size_t)sn * a.ld + ch] : (uint16_t)0;
+            wt[u][k] = sn >= 0 ? nv_s[sn][tid] : (uint16_t)0;
           }
       }
 #pragma unroll
