@@ -52,9 +52,6 @@ constexpr int kGdnMaxM = 8;  // tokens per chain step (the reference's MP, fused
 constexpr int kGdnMaxTree = 32;  // nodes per draft-tree step
 // tokens per conv workgroup of the prep: all of a chain step's, 4 of a larger tree's
 template <int MAXM> constexpr int gdn_tg() { return MAXM <= 8 ? 8 : 4; }
-// A workgroup barrier that orders LDS accesses only: __syncthreads' workgroup fence also waits
-// for the wave's global loads still in flight, which the prep's early loads must not.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 constexpr int kGdnThreads = 256;
 static_assert(kGdnBV == 16, "the step kernel's lane layout: 8 column pairs");
 

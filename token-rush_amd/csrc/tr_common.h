@@ -110,6 +110,11 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
   return r;
 }
 
+// A workgroup barrier that orders LDS accesses only. __syncthreads' workgroup fence also makes
+// the wave wait for its global memory operations still in flight (loads issued ahead, stores
+// not yet acknowledged), which a barrier guarding LDS alone does not need.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Cross-lane sums on the VALU (DPP and the gfx950 permlane swaps) instead of LDS-routed
 // ds_bpermute shuffles. Each returns, in every lane, the sum over the lanes of its group; the
 // two lanes of a pair add the same two values (a + b == b + a), so every lane of a group ends
