@@ -238,7 +238,7 @@ __device__ __forceinline__ int udiv_small(uint32_t q, int d, uint32_t magic) {
 
 // One accumulator tile element: (mt, lane, r) -> output row m = 16 mt + 4 (lane / 16) + r,
 // column n = 16 strip + lane % 16.
-template <int MT, int GW, bool F16S, bool XDMA>
+template <int MT, int GW, bool F16S, bool XSTAGE>
 __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // 16-byte aligned: the dynamic area follows the kernel's 776 bytes of static LDS, and the
   // ring's and staging area's 16-byte accesses stall when misaligned (SQ_LDS_UNALIGNED_STALL)
@@ -286,18 +286,19 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // A-operand layout (lane l: row l % 16 of its row tile, k = 32 j + 8 (l / 16) .. + 7 of MFMA j).
   // Padding groups (g >= G) read group G - 1: finite values that meet zero scale and min.
   uint4 xa[GW][MT][4];
-  if constexpr (XDMA) {
-    // M <= 8: load the rows coalesced straight into this wave's LDS staging area
-    // (buffer_load ... lds, no VGPRs), then read them back in the operand layout. In the operand
-    // layout itself consecutive lanes would read different rows, each lane a separate cache
-    // access, which took 3-6 us for these 8 KB per wave. Load t brings row t of the wave's four
+  uint4 xv[8];  // staged rows, held in VGPRs until they are written to LDS
+  if constexpr (XSTAGE) {
+    // M <= 8: load the rows coalesced into VGPRs, write them to this wave's LDS staging area,
+    // then read them back in the operand layout. In the operand layout itself consecutive lanes
+    // would read different rows, each lane a separate cache access, which took 3-6 us for these
+    // 8 KB per wave. Loading straight into LDS (buffer_load ... lds) lands no earlier and made the
+    // M = 8 layer set 0.8 us slower than this register round trip. Load t brings row t of the wave's four
     // groups (lane l: group l / 16, 16-byte chunk (l % 16) ^ t), so a call issues M loads, one per
     // real row: every load instruction costs the CU's address unit the same 16 cycles whether
     // its lanes fetch or not. The staging area holds row r of group gw at (r GW + gw) 256 bytes,
     // chunk k of the row in 16-byte slot k ^ r, so the 16 rows read by one operand load fall in
     // different LDS banks.
     static_assert(MT == 1 && GW == 4, "activation staging covers one row tile and four groups");
-    char* stage = (char*)red + a.xstage_off + wave * (GW * 2048);
     const auto xrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.M * a.K * 2, 0x00020000);
     const int lk = lane & 15;
     const int g = min(gbase + (lane >> 4), G - 1);
@@ -305,8 +306,8 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     for (int t = 0; t < 8; ++t) {
       if (t >= a.M) break;
       const int off = (t * a.K + g * kGroup) * 2 + ((lk ^ t) & 15) * 16;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void*)(stage + t * 1024), 16, off,
-                                               0, 0, 0);
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+      xv[t] = make_uint4(v.x, v.y, v.z, v.w);
     }
   } else {
 #pragma unroll
@@ -329,15 +330,20 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // before any wave's weight requests, so no wave waits for its activations behind the other
   // waves' strips.
   TLM(21);
-  if constexpr (XDMA) __builtin_amdgcn_s_barrier();
+  if constexpr (XSTAGE) __builtin_amdgcn_s_barrier();
   TLM(22);
   load_strip<GW>(buf[0], rsrc, active ? strip_off(r0) : oob, lane_off, sm_voff);
   load_strip<GW>(buf[1], rsrc, active ? strip_off(r0 + 1) : oob, lane_off, sm_voff);
   TLM(3);
-  if constexpr (XDMA) {
+  if constexpr (XSTAGE) {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (GW + 1)) : "memory");  // the staging loads have landed
     TLM(2);
-    const char* stage = (const char*)red + a.xstage_off + wave * (GW * 2048);
+    char* stage = (char*)red + a.xstage_off + wave * (GW * 2048);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (t >= a.M) break;
+      *(uint4*)(stage + t * 1024 + lane * 16) = xv[t];  // lane l: chunk l % 16 of group l / 16
+    }
     const int i = lane & 15;
 #pragma unroll
     for (int gw = 0; gw < GW; ++gw) {
@@ -778,7 +784,7 @@ bool make_plan(int N, int K, int M, int S_req, int R_req, Plan* p) {
   return true;
 }
 
-template <int MT, int GW, bool F16S, bool XDMA>
+template <int MT, int GW, bool F16S, bool XSTAGE>
 hipError_t launch_t(GemmArgs a, const Plan& p, hipStream_t stream) {
   const dim3 grid(p.grid_n * p.S), block(64 * p.W);
   const size_t per_strip = (size_t)p.W * MT * 256 * sizeof(float);
@@ -786,24 +792,24 @@ hipError_t launch_t(GemmArgs a, const Plan& p, hipStream_t stream) {
   // the CU's LDS among the workgroups the plan puts on one CU, so larger batches never cost
   // occupancy.
   const int wg_per_cu = p.W >= kWavesPerCU ? 1 : kWavesPerCU / p.W;
-  int rb = (int)((XDMA ? kLdsBudget : kLdsMax / wg_per_cu) / (2 * per_strip));
+  int rb = (int)((XSTAGE ? kLdsBudget : kLdsMax / wg_per_cu) / (2 * per_strip));
   a.RB = rb < 1 ? 1 : (rb > 4 ? 4 : rb);
   const size_t ring = 2 * a.RB * per_strip;
   a.xstage_off = (int)ring;
-  const size_t lds = XDMA ? ring + (size_t)p.W * GW * 2048 : ring;
+  const size_t lds = XSTAGE ? ring + (size_t)p.W * GW * 2048 : ring;
   {
     // staging + ring, or a ring over 64 KB, exceed the default 64 KB of dynamic LDS: raise this
     // kernel's limit once
     static bool raised = false;
     if (!raised) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&int4_gemm_kernel<MT, GW, F16S, XDMA>),
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&int4_gemm_kernel<MT, GW, F16S, XSTAGE>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
       if (e != hipSuccess) return e;
       raised = true;
     }
     if (lds > kLdsMax) return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL((int4_gemm_kernel<MT, GW, F16S, XDMA>), grid, block, lds, stream, a);
+  hipLaunchKernelGGL((int4_gemm_kernel<MT, GW, F16S, XSTAGE>), grid, block, lds, stream, a);
   return hipGetLastError();
 }
 
