@@ -228,7 +228,7 @@ struct GemmArgs {
   int* am_cnt;            // arrival counter, zero between calls
   const int64_t* spec;    // [M] committed token + drafts, or null (argmax only)
   AcceptOut o;            // o.pred [M] always; the rest when spec != null
-  int xstage_off;         // byte offset of the activation staging area in dynamic LDS (M <= 8)
+  int xstage_off;         // byte offset of the activation staging area in dynamic LDS (M <= 8, M > 16)
 };
 
 // q / d for q < 2^16 and 1 <= d < 2^15, magic = ceil(2^32 / d) (d == 1 has no 32-bit magic).
@@ -286,7 +286,8 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   // A-operand layout (lane l: row l % 16 of its row tile, k = 32 j + 8 (l / 16) .. + 7 of MFMA j).
   // Padding groups (g >= G) read group G - 1: finite values that meet zero scale and min.
   uint4 xa[GW][MT][4];
-  uint4 xv[8];  // staged rows, held in VGPRs until they are written to LDS
+  constexpr int kXL = MT == 1 ? 8 : 16;  // staging loads per wave: one per row (GW = 4), or per row pair (GW = 2)
+  uint4 xv[kXL];                         // staged rows, held in VGPRs until they are written to LDS
   if constexpr (XSTAGE) {
     // M <= 8: load the rows coalesced into VGPRs, write them to this wave's LDS staging area,
     // then read them back in the operand layout. In the operand layout itself consecutive lanes
@@ -298,16 +299,33 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     // its lanes fetch or not. The staging area holds row r of group gw at (r GW + gw) 256 bytes,
     // chunk k of the row in 16-byte slot k ^ r, so the 16 rows read by one operand load fall in
     // different LDS banks.
-    static_assert(MT == 1 && GW == 4, "activation staging covers one row tile and four groups");
+    //
+    // M = 17..32 (two row tiles, two groups per wave): load u brings rows 2u and 2u + 1 (lanes
+    // 0-31 and 32-63; lane l: group (l / 16) % 2, chunk (l % 16) ^ (row % 16)), all 16 loads
+    // issued before the strips, and the 16-row tiles are staged one after the other through the
+    // same 8 KB per wave. That area lies inside the reduction ring, which is first written after
+    // the prologue (an LDS barrier orders them). Rows >= M load from beyond the resource: zeros.
+    static_assert((MT == 1 && GW == 4) || (MT == 2 && GW == 2), "activation staging: 1 x 4 or 2 x 2 tiles");
     const auto xrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.M * a.K * 2, 0x00020000);
     const int lk = lane & 15;
-    const int g = min(gbase + (lane >> 4), G - 1);
+    if constexpr (MT == 1) {
+      const int g = min(gbase + (lane >> 4), G - 1);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      if (t >= a.M) break;
-      const int off = (t * a.K + g * kGroup) * 2 + ((lk ^ t) & 15) * 16;
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
-      xv[t] = make_uint4(v.x, v.y, v.z, v.w);
+      for (int t = 0; t < 8; ++t) {
+        if (t >= a.M) break;
+        const int off = (t * a.K + g * kGroup) * 2 + ((lk ^ t) & 15) * 16;
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+        xv[t] = make_uint4(v.x, v.y, v.z, v.w);
+      }
+    } else {
+      const int g = min(gbase + ((lane >> 4) & 1), G - 1);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int row = 2 * u + (lane >> 5);
+        const int off = row < a.M ? (row * a.K + g * kGroup) * 2 + ((lk ^ row) & 15) * 16 : 0x7FFFFFF0;
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+        xv[u] = make_uint4(v.x, v.y, v.z, v.w);
+      }
     }
   } else {
 #pragma unroll
@@ -338,22 +356,32 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
   if constexpr (XSTAGE) {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (GW + 1)) : "memory");  // the staging loads have landed
     TLM(2);
-    char* stage = (char*)red + a.xstage_off + wave * (GW * 2048);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      if (t >= a.M) break;
-      *(uint4*)(stage + t * 1024 + lane * 16) = xv[t];  // lane l: chunk l % 16 of group l / 16
-    }
+    char* stage = (char*)red + a.xstage_off + wave * (GW * 256 * (MT == 1 ? 8 : 16));
     const int i = lane & 15;
 #pragma unroll
-    for (int gw = 0; gw < GW; ++gw) {
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (MT == 1) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = 4 * j + (lane >> 4);
-        const uint4 v = *(const uint4*)(stage + ((i & 7) * GW + gw) * 256 + ((k ^ i) & 15) * 16);
-        xa[gw][0][j] = i < a.M ? v : make_uint4(0u, 0u, 0u, 0u);
+        for (int t = 0; t < 8; ++t) {
+          if (t >= a.M) break;
+          *(uint4*)(stage + t * 1024 + lane * 16) = xv[t];  // lane l: chunk l % 16 of group l / 16
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) *(uint4*)(stage + u * 1024 + lane * 16) = xv[8 * mt + u];  // rows 2u, 2u + 1
+      }
+#pragma unroll
+      for (int gw = 0; gw < GW; ++gw) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = 4 * j + (lane >> 4);
+          const int rs = MT == 1 ? (i & 7) : i;  // staged row
+          const uint4 v = *(const uint4*)(stage + (rs * GW + gw) * 256 + ((k ^ i) & 15) * 16);
+          xa[gw][mt][j] = 16 * mt + i < a.M ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
       }
     }
+    if constexpr (MT == 2) lds_barrier();  // every wave's staging reads before any ring write
   }
 
   // Xa[mt] = sum of x over group gbase + lane / 16 for row 16 mt + lane % 16 (the A operand of
@@ -791,12 +819,15 @@ hipError_t launch_t(GemmArgs a, const Plan& p, hipStream_t stream) {
   // Ring budget: the staged kernel keeps 64 KB (its staging takes the rest); the others share
   // the CU's LDS among the workgroups the plan puts on one CU, so larger batches never cost
   // occupancy.
+  // The two-tile staging area shares the ring (it is dead before the first partial is written).
+  constexpr bool kShared = XSTAGE && MT == 2;
   const int wg_per_cu = p.W >= kWavesPerCU ? 1 : kWavesPerCU / p.W;
-  int rb = (int)((XSTAGE ? kLdsBudget : kLdsMax / wg_per_cu) / (2 * per_strip));
+  int rb = (int)(((XSTAGE && !kShared) ? kLdsBudget : kLdsMax / wg_per_cu) / (2 * per_strip));
   a.RB = rb < 1 ? 1 : (rb > 4 ? 4 : rb);
   const size_t ring = 2 * a.RB * per_strip;
-  a.xstage_off = (int)ring;
-  const size_t lds = XSTAGE ? ring + (size_t)p.W * GW * 2048 : ring;
+  const size_t stage = XSTAGE ? (size_t)p.W * GW * 256 * (MT == 1 ? 8 : 16) : 0;
+  a.xstage_off = kShared ? 0 : (int)ring;
+  const size_t lds = kShared ? (ring > stage ? ring : stage) : ring + stage;
   {
     // staging + ring, or a ring over 64 KB, exceed the default 64 KB of dynamic LDS: raise this
     // kernel's limit once
@@ -815,7 +846,7 @@ hipError_t launch_t(GemmArgs a, const Plan& p, hipStream_t stream) {
 
 hipError_t launch(const GemmArgs& a, const Plan& p, int scale_dtype, hipStream_t stream) {  // NOLINT
   const bool f16 = scale_dtype == 1;
-  if (a.M > 16) return f16 ? launch_t<2, 2, true, false>(a, p, stream) : launch_t<2, 2, false, false>(a, p, stream);
+  if (a.M > 16) return f16 ? launch_t<2, 2, true, true>(a, p, stream) : launch_t<2, 2, false, true>(a, p, stream);
   if (a.M <= 8) return f16 ? launch_t<1, 4, true, true>(a, p, stream) : launch_t<1, 4, false, true>(a, p, stream);
   return f16 ? launch_t<1, 4, true, false>(a, p, stream) : launch_t<1, 4, false, false>(a, p, stream);
 }
