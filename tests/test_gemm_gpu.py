@@ -55,7 +55,7 @@ def test_pack_matches_oracle(dev, N, K):
 
 @pytest.mark.parametrize("N,K", [(5120, 6144), (256, 5120), (1280, 5120), (14336, 5120), (5120, 17408),
                                  (256, 384), (1280, 2176), (512, 128)])
-@pytest.mark.parametrize("M", [1, 3, 8, 16])
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 13, 16])
 def test_mul_matches_oracle(dev, N, K, M):
     from tokenrush_amd import gfx950
     say(f"mul N={N} K={K} M={M}")
@@ -305,10 +305,11 @@ def _config2_case(N, K):
 
 
 @pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
-@pytest.mark.parametrize("M", [2, 4, 24, 32])
+@pytest.mark.parametrize("M", [2, 4, 12, 24, 32])
 def test_config2_shapes_m_sweep(dev, N, K, M):
-    """The bench's M sweep (config 2 at M = 2, 4) and config 4's M = 32 verify GEMM (with
-    M = 24 between the row-tile boundaries) on every config-2 shape against float64."""
+    """The bench's M sweep (config 2 at M = 2, 4), a 12-row call (the one-tile kernel's second
+    staging pass) and config 4's M = 32 verify GEMM (with M = 24 between the row-tile boundaries)
+    on every config-2 shape against float64."""
     from tokenrush_amd import gfx950
     say(f"config2 sweep N={N} K={K} M={M}")
     B, sp, mp, W = _config2_case(N, K)
