@@ -131,6 +131,20 @@ def test_rows_independent_of_m(dev):
         assert torch.equal(gfx950.mul(x[:M].contiguous(), B, sp, mp), y32[:M]), M
 
 
+@pytest.mark.parametrize("N,K", [(512, 128), (16, 384), (1280, 2176), (48, 5120)])
+@pytest.mark.parametrize("M", [17, 25, 31])
+def test_two_row_tiles_small_and_odd_k(dev, N, K, M):
+    """Above 16 rows the activations are staged in two 16-row passes through an LDS area shared
+    with the reduction ring: one group (K = 128, padded to a quad), an odd group count
+    (K = 2176), one strip (N = 16) and rows past M in both tiles, against float64."""
+    from tokenrush_amd import gfx950
+    say(f"two tiles small N={N} K={K} M={M}")
+    p, s, m = o.make_weights(N, K, seed=40 + M, dtype="bf16")
+    x = o.make_x(M, K, seed=41 + M)
+    B, sp, mp = gfx950.pack(*dev_weights(p, s, m, "bf16"))
+    check_close(gfx950.mul(dev_x(x), B, sp, mp), x.astype(np.float64) @ o.weights_f64(p, s, m).T, f"N={N} K={K} M={M}")
+
+
 def test_repeat_is_deterministic(dev):
     from tokenrush_amd import gfx950
     say("determinism")
