@@ -90,14 +90,16 @@ def test_tree_split_count_fits_one_pass():
 
 def test_partial_plan_is_host_only_and_independent_of_m():
     """The partial-mode plan (the caller sums the slots): between the out-mode plan's slot
-    count and 6, depending on M only through the row-tile range, and the slot counts measured
-    fastest for the o and down projections (3 and 4 below 17 rows)."""
+    count and 6, depending on M only through the kernel's row range (1-8 staged, 9-16, 17-32),
+    and the slot counts measured fastest for the o and down projections (3 at every M; down 5
+    up to 8 rows, 4 at 9-16, 6 above)."""
     from tokenrush_amd import gfx950
     for N, K in [(5120, 5120), (7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (16, 128), (512, 17408)]:
-        for M in (1, 8, 16, 17, 32):
+        for M in (1, 8, 9, 16, 17, 32):
             S = gfx950.partial_slots(N, K, M)
             S0 = gfx950.plan(N, K, M)[0]
             assert S0 <= S <= max(S0, 6), (N, K, M, S, S0)
-            assert gfx950.partial_slots(N, K, 1 if M <= 16 else 32) == S
-    assert gfx950.partial_slots(5120, 6144, 8) == 3 and gfx950.partial_slots(5120, 17408, 8) == 4
+            assert gfx950.partial_slots(N, K, 1 if M <= 8 else (16 if M <= 16 else 32)) == S
+    assert [gfx950.partial_slots(5120, 6144, M) for M in (1, 8, 16, 32)] == [3, 3, 3, 3]
+    assert [gfx950.partial_slots(5120, 17408, M) for M in (1, 8, 16, 32)] == [5, 5, 4, 6]
     assert gfx950.partial_slots(5120, 17408, 32) == gfx950.plan(5120, 17408, 32)[0] == 6

@@ -765,9 +765,14 @@ bool make_plan(int N, int K, int M, int S_req, int R_req, Plan* p);
 
 // The partial-mode plan (the caller sums the slots, so more K slots cost only their writes, not
 // a last-arriver slot sum): the slot count from the default's up to 6 with the least work on the
-// busiest CU, ceil(workgroups / CUs) x strips x waves, the smaller count on ties. Measured at
-// M = 8 (graph of launches, us): the 5120 x 6144 projection 7.62 at the default 1 slot, 6.72 at
-// the chosen 3; 5120 x 17408 12.38 at 3, 12.0 at the chosen 4.
+// busiest CU, rounds of workgroups x strips x waves, the smaller count on ties. The staged M <= 8
+// kernel also counts its prologue (activation staging and group sums, ending ~4.7 us after launch
+// against ~1.2 us per strip) as kRampStrips strips per workgroup, which favours fewer waves per
+// workgroup. Measured at M = 8 (graph of launches, us): the 5120 x 6144 projection 7.31 at 1
+// slot, 9.55 at 2, 6.54 at the chosen 3, 7.43 at 4; 5120 x 17408 12.35 at 3, 11.93 at 4, 11.67
+// at the chosen 5, 13.96 at 6 (M = 1: 11.6, 11.7, 10.47, 12.3). At M = 16 (unstaged) 5120 x 17408
+// ran 14.13 at 4 and 14.35 at 5 slots, and keeps 4.
+constexpr long kRampStrips = 3;
 bool make_partial_plan(int N, int K, int M, Plan* p) {
   Plan best;
   if (!make_plan(N, K, M, 0, 0, &best)) return false;
@@ -777,7 +782,8 @@ bool make_partial_plan(int N, int K, int M, Plan* p) {
     Plan q;
     if (!make_plan(N, K, M, S, 0, &q)) continue;
     const long grid = (long)q.grid_n * q.S;
-    const long cost = (grid + kCUs - 1) / kCUs * q.R * q.W;
+    const long rounds = (grid + kCUs - 1) / kCUs;
+    const long cost = rounds * (q.R + (M <= 8 ? kRampStrips : 0)) * q.W;
     if (best_cost < 0 || cost < best_cost) {
       best_cost = cost;
       best = q;

@@ -255,7 +255,7 @@ _slots = {}
 def partial_slots(N: int, K: int, M: int = 1) -> int:
     """fp32 slots mul_partial writes for an N x K weight at M rows
     (marlin.partial_slots, marlin.py:151-155)."""
-    key = (N, K, M > 16)
+    key = (N, K, 0 if M <= 8 else (1 if M <= 16 else 2))  # the plan depends on M through these ranges
     if key not in _slots:
         S = ext().tr_partial_slots(N, K, M)
         if S < 1:
