@@ -346,7 +346,8 @@ def config4_tree_step(torch, dev, model, reps=10, M=32):
 TL_MARKS = {0: "entry", 1: "launch constants", 21: "activation loads issued", 22: "past the ordering barrier",
             3: "first two strips issued", 2: "activations staged",
             4: "prologue end", 5: "strip 0 MACs", 6: "strip 1 MACs", 7: "strip 2 MACs", 8: "strip 3 MACs",
-            9: "strip 4 MACs", 10: "strip 5 MACs", 16: "batch reduced (last)", 20: "strip loop exit"}
+            9: "strip 4 MACs", 10: "strip 5 MACs", 16: "batch reduced (last)", 20: "strip loop exit",
+            19: "slot-sum arrival (K slots > 1)", 23: "slot sum done (last arriver)"}
 
 
 def gemm_timeline(torch, gfx950, dev, name, M=M_VERIFY, launches=6):

@@ -553,16 +553,16 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
     if (last) handoff_acquire();
   }
   __syncthreads();
+  TLM(19);
   if (!last) return;
-  // Each thread takes kTailE outputs per pass (two sums each in the pair layout: gate and up)
-  // and loads their partials kTailS slots at a time, all loads of a step issued together
-  // (outputs past the range load the last output's partials and store nothing), then adds them
-  // in slot order. A loop of dependent loads here waited for each partial in turn.
-  const int F = a.N / 2;
+  // Each thread takes kTailE outputs per pass and loads their partials kTailS slots at a time,
+  // all loads of a step issued together (outputs past the range load the last output's partials
+  // and store nothing), then adds them in slot order. A loop of dependent loads here waited for
+  // each partial in turn. (The pair layout's silu outputs take slot_sum_kernel instead.)
   const int nstr = r1 - r0;
-  const int j = threadIdx.x & (a.silu ? 7 : 15);
+  const int j = threadIdx.x & 15;
   const size_t slot_stride = (size_t)a.M * a.N;
-  for (StripWalk w = a.silu ? walk8 : walk16; w.s < nstr;) {
+  for (StripWalk w = walk16; w.s < nstr;) {
     int mi[kTailE], ni[kTailE];
     size_t off[kTailE];
     bool live[kTailE];
@@ -574,45 +574,76 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
       off[i] = (size_t)mi[i] * a.N + ni[i];
       w.next();
     }
-    float v[kTailE][2];
+    float v[kTailE];
 #pragma unroll
-    for (int i = 0; i < kTailE; ++i) v[i][0] = v[i][1] = 0.f;
+    for (int i = 0; i < kTailE; ++i) v[i] = 0.f;
     for (int s0 = 0; s0 < a.S; s0 += kTailS) {
-      float p[kTailS][kTailE][2];
+      float p[kTailS][kTailE];
 #pragma unroll
       for (int q = 0; q < kTailS; ++q) {
         const float* base = a.ws_part + (size_t)min(s0 + q, a.S - 1) * slot_stride;
 #pragma unroll
-        for (int i = 0; i < kTailE; ++i) {
-          p[q][i][0] = __hip_atomic_load(base + off[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          p[q][i][1] = a.silu ? __hip_atomic_load(base + off[i] + 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-        }
+        for (int i = 0; i < kTailE; ++i) p[q][i] = __hip_atomic_load(base + off[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
 #pragma unroll
       for (int q = 0; q < kTailS; ++q)
 #pragma unroll
         for (int i = 0; i < kTailE; ++i)
-          if (s0 + q < a.S) {
-            v[i][0] += p[q][i][0];
-            v[i][1] += p[q][i][1];
-          }
+          if (s0 + q < a.S) v[i] += p[q][i];
     }
 #pragma unroll
     for (int i = 0; i < kTailE; ++i) {
       if (!live[i]) break;
-      const size_t m = mi[i];
-      const int n = ni[i];
-      if (a.silu) {
-        const float g = bf16_bits_to_f32(f32_to_bf16_bits(v[i][0]));
-        const float u = bf16_bits_to_f32(f32_to_bf16_bits(v[i][1]));
-        ((uint16_t*)a.out)[m * F + (n >> 4) * 8 + j] = f32_to_bf16_bits(silu_mul_f32(g, u));
-      } else {
-        ((uint16_t*)a.out)[m * a.N + n] = f32_to_bf16_bits(v[i][0]);
-      }
+      ((uint16_t*)a.out)[(size_t)mi[i] * a.N + ni[i]] = f32_to_bf16_bits(v[i]);
     }
   }
+  TLM(23);
   if (threadIdx.x == 0)
     __hip_atomic_store(a.ws_cnt + rbi * kWsCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The gate/up pair layout with more than one K slot: the slots' fp32 partials [S, M, N] summed in
+// slot order, four outputs per thread; output (m, 8 s + j) is silu(bf16(g)) * bf16(u) with g, u
+// the sums of columns 16 s + j and 16 s + 8 + j (the epilogue's arithmetic). A second launch
+// instead of the GEMM's last-arriver sum: that tail loads two partials per output, and at M = 32
+// gate_up took 37.2-37.6 us with it against 35.0 us for partials plus this kernel. Plain out mode
+// keeps the in-kernel sum (qkv 12.8-13.1 us with it, 13.1-14.3 us with a second launch).
+__global__ __launch_bounds__(256) void slot_sum_kernel(const float* __restrict__ part, int S, int M, int N, int silu,
+                                                       uint16_t* __restrict__ out) {
+  const size_t slot = (size_t)M * N;
+  const int F = N / 2;
+  const size_t quads = (silu ? (size_t)M * F : (size_t)M * N) / 4;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < quads; i += (size_t)gridDim.x * blockDim.x) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f), w = v;
+    size_t off;
+    if (silu) {
+      const size_t m = 4 * i / F;
+      const int c = (int)(4 * i % F), sb = c >> 3, j = c & 7;  // j = 0 or 4
+      off = m * N + 16 * sb + j;
+    } else {
+      off = 4 * i;
+    }
+    for (int q = 0; q < S; ++q) {
+      const float4 p = *(const float4*)(part + q * slot + off);
+      v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+      if (silu) {
+        const float4 r = *(const float4*)(part + q * slot + off + 8);
+        w.x += r.x; w.y += r.y; w.z += r.z; w.w += r.w;
+      }
+    }
+    uint2 o;
+    if (silu) {
+      const float g[4] = {v.x, v.y, v.z, v.w}, u[4] = {w.x, w.y, w.z, w.w};
+      uint32_t b[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        b[e] = f32_to_bf16_bits(silu_mul_f32(bf16_bits_to_f32(f32_to_bf16_bits(g[e])), bf16_bits_to_f32(f32_to_bf16_bits(u[e]))));
+      o = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+    } else {
+      o = make_uint2(f32_to_bf16_bits(v.x) | (f32_to_bf16_bits(v.y) << 16), f32_to_bf16_bits(v.z) | (f32_to_bf16_bits(v.w) << 16));
+    }
+    *(uint2*)(out + 4 * i) = o;
+  }
 }
 
 // ----------------------------------------------------------------------------- layout kernels
@@ -957,6 +988,19 @@ static int gemm_impl(const void* x, const void* packed, void* out, void* partial
     const size_t need = ws_counter_bytes() + (size_t)p.S * M * N * sizeof(float);
     if (!workspace || workspace_bytes < need) return TR_ERR_ARG;
     if (p.grid_n > kWsCounters) return TR_ERR_CONFIG;
+    if (silu) {
+      // the K slots' partials into the workspace, then their sum and silu in a second launch
+      float* part = (float*)((char*)workspace + ws_counter_bytes());
+      a.mode = OUT_PARTIAL;
+      a.out = part;
+      a.silu = 0;
+      if (launch(a, p, scale_dtype, (hipStream_t)stream) != hipSuccess) return TR_ERR_LAUNCH;
+      const size_t quads = (size_t)M * (N / 2) / 4;
+      const int blocks = (int)((quads + 255) / 256 < 2048 ? (quads + 255) / 256 : 2048);
+      hipLaunchKernelGGL(slot_sum_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, part, p.S, M, N, 1,
+                         (uint16_t*)out);
+      return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
+    }
     a.mode = OUT_BF16_VIA_WS;
     a.out = out;
     a.ws_cnt = (int*)workspace;
