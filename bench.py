@@ -337,7 +337,7 @@ def config4_tree_step(torch, dev, model, reps=10, M=32):
     t = sum(times) / len(times)
     return {"ms_per_step": round(t * 1e3, 3), "M": M, "replays": reps,
             "accepted_depth": sorted(set(accepted)), "planted_depth": len(path) - 1,
-            "note": "one hipGraph: 257 int4 GEMMs at M=32, tree GDN steps (per-node state, 32 snapshot slots), "
+            "note": "one hipGraph: 257 int4 GEMMs at M=32 (the 64 gate/up GEMMs then slot_sum_kernel for their two K slots and silu), tree GDN steps (per-node state, 32 snapshot slots), "
                     "ancestor-masked FP8 attention over 8192 live tokens, lm_head 248320x5120 writing logits, tree "
                     "accept, commit of KV rows/scales (4 launches) and conv rings (1 launch); node tokens planted "
                     "along the deepest root path, each replay from the same restored state"}
