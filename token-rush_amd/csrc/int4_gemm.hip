@@ -608,41 +608,27 @@ __global__ __launch_bounds__(768) void int4_gemm_kernel(GemmArgs a) {
 // instead of the GEMM's last-arriver sum: that tail loads two partials per output, and at M = 32
 // gate_up took 37.2-37.6 us with it against 35.0 us for partials plus this kernel. Plain out mode
 // keeps the in-kernel sum (qkv 12.8-13.1 us with it, 13.1-14.3 us with a second launch).
-__global__ __launch_bounds__(256) void slot_sum_kernel(const float* __restrict__ part, int S, int M, int N, int silu,
+__global__ __launch_bounds__(256) void slot_sum_kernel(const float* __restrict__ part, int S, int M, int N,
                                                        uint16_t* __restrict__ out) {
   const size_t slot = (size_t)M * N;
   const int F = N / 2;
-  const size_t quads = (silu ? (size_t)M * F : (size_t)M * N) / 4;
+  const size_t quads = (size_t)M * F / 4;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < quads; i += (size_t)gridDim.x * blockDim.x) {
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f), w = v;
-    size_t off;
-    if (silu) {
-      const size_t m = 4 * i / F;
-      const int c = (int)(4 * i % F), sb = c >> 3, j = c & 7;  // j = 0 or 4
-      off = m * N + 16 * sb + j;
-    } else {
-      off = 4 * i;
-    }
+    const size_t m = 4 * i / F;
+    const int c = (int)(4 * i % F), sb = c >> 3, j = c & 7;  // j = 0 or 4
+    const size_t off = m * N + 16 * sb + j;
+    float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
     for (int q = 0; q < S; ++q) {
-      const float4 p = *(const float4*)(part + q * slot + off);
-      v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
-      if (silu) {
-        const float4 r = *(const float4*)(part + q * slot + off + 8);
-        w.x += r.x; w.y += r.y; w.z += r.z; w.w += r.w;
-      }
+      const float4 p = *(const float4*)(part + q * slot + off), r = *(const float4*)(part + q * slot + off + 8);
+      g.x += p.x; g.y += p.y; g.z += p.z; g.w += p.w;
+      u.x += r.x; u.y += r.y; u.z += r.z; u.w += r.w;
     }
-    uint2 o;
-    if (silu) {
-      const float g[4] = {v.x, v.y, v.z, v.w}, u[4] = {w.x, w.y, w.z, w.w};
-      uint32_t b[4];
+    const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+    uint32_t b[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        b[e] = f32_to_bf16_bits(silu_mul_f32(bf16_bits_to_f32(f32_to_bf16_bits(g[e])), bf16_bits_to_f32(f32_to_bf16_bits(u[e]))));
-      o = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
-    } else {
-      o = make_uint2(f32_to_bf16_bits(v.x) | (f32_to_bf16_bits(v.y) << 16), f32_to_bf16_bits(v.z) | (f32_to_bf16_bits(v.w) << 16));
-    }
-    *(uint2*)(out + 4 * i) = o;
+    for (int e = 0; e < 4; ++e)
+      b[e] = f32_to_bf16_bits(silu_mul_f32(bf16_bits_to_f32(f32_to_bf16_bits(gv[e])), bf16_bits_to_f32(f32_to_bf16_bits(uv[e]))));
+    *(uint2*)(out + 4 * i) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
   }
 }
 
@@ -997,7 +983,7 @@ static int gemm_impl(const void* x, const void* packed, void* out, void* partial
       if (launch(a, p, scale_dtype, (hipStream_t)stream) != hipSuccess) return TR_ERR_LAUNCH;
       const size_t quads = (size_t)M * (N / 2) / 4;
       const int blocks = (int)((quads + 255) / 256 < 2048 ? (quads + 255) / 256 : 2048);
-      hipLaunchKernelGGL(slot_sum_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, part, p.S, M, N, 1,
+      hipLaunchKernelGGL(slot_sum_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, part, p.S, M, N,
                          (uint16_t*)out);
       return hipGetLastError() == hipSuccess ? TR_OK : TR_ERR_LAUNCH;
     }
