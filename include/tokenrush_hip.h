@@ -70,7 +70,9 @@ int tr_int4_gemm_noalloc(const void* x, const void* packed, void* out, int M, in
 /* Fused gate/up + activation: packed is a [gate (N/2 rows); up (N/2 rows)] weight packed by
  * tr_pack_int4_pairs; out bf16 [M, N/2] = silu(bf16(x . gate^T)) * bf16(x . up^T), bit for bit what
  * tr_int4_gemm followed by tr_silu_mul produce. N % 32 == 0; workspace as for tr_int4_gemm.
- * Replaces: silu_mul(gate_up(n)) (tokenrush/model.py:156-160, tokenrush/fused.py:67-87) in one launch. */
+ * Replaces: silu_mul(gate_up(n)) (tokenrush/model.py:156-160, tokenrush/fused.py:67-87) in one launch, or
+ * two when the plan takes more than one K slot (M > 16 at K = 5120): the K slots' partials into the
+ * workspace, then their in-order sum and the activation. */
 int tr_int4_gemm_silu(const void* x, const void* packed, void* out, void* workspace, size_t workspace_bytes, int M,
                       int N, int K, int group, int scale_dtype, void* stream);
 
